@@ -1,0 +1,252 @@
+/*
+ * nvdsa.h — C ABI of the MI355X (gfx950) DSA stable-decode offload chain.
+ *
+ * Seven entry points replace the seven torch.library operators that the
+ * reference registers under the `nanovllm_dsa` namespace
+ * (reference: csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:645-696).
+ * Each takes its arguments in the same order as the reference schema, as
+ * plain tensor descriptors (device address + dtype + shape), plus the HIP
+ * stream to launch on.  Every entry point:
+ *   - validates shapes / dtypes / layout exactly as the reference adapter's
+ *     TORCH_CHECKs do and returns a non-zero nvdsa_status with a message
+ *     (nvdsa_last_error) instead of throwing;
+ *   - never allocates device memory: scratch space is a caller-provided
+ *     workspace whose size the matching *_workspace_size call reports
+ *     (the counterpart of aclnnXGetWorkspaceSize + the adapter's workspace
+ *     allocation in common/torch_adapter/op_api_common.h:565-600);
+ *   - never synchronises the host; it enqueues kernels on `stream` only, so
+ *     a sequence of calls is capturable into a HIP graph;
+ *   - skips invalid rows silently on the device (zero miss count, zero
+ *     attention output, skipped copy pair), as the reference kernels do.
+ *
+ * All entry points are safe to call from several host threads; the error
+ * message is thread-local.
+ */
+#ifndef NVDSA_H
+#define NVDSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+typedef enum nvdsa_status {
+  NVDSA_OK = 0,
+  NVDSA_ERR_SHAPE = 1,     /* rank / extent mismatch */
+  NVDSA_ERR_DTYPE = 2,     /* element type not accepted */
+  NVDSA_ERR_LAYOUT = 3,    /* not contiguous or misaligned */
+  NVDSA_ERR_DEVICE = 4,    /* tensors on different devices */
+  NVDSA_ERR_WORKSPACE = 5, /* workspace missing or too small */
+  NVDSA_ERR_RUNTIME = 6,   /* HIP runtime error while launching */
+  NVDSA_ERR_ARG = 7        /* null pointer / bad scalar argument */
+} nvdsa_status;
+
+/* Element types. */
+typedef enum nvdsa_dtype {
+  NVDSA_INT32 = 0,
+  NVDSA_FLOAT16 = 1,
+  NVDSA_BFLOAT16 = 2,
+  NVDSA_FLOAT32 = 3
+} nvdsa_dtype;
+
+/* Device ordinal value for pinned host memory that is mapped into the GPU
+ * address space (the counterpart of torch_npu.empty_with_swapped_memory,
+ * reference nanovllm/engine/model_runner.py:651-652).  Only the two DRAM
+ * cache arguments of the copy entry points accept it. */
+#define NVDSA_HOST_MAPPED_DEVICE (-1)
+
+/* A dense tensor: `data` is an address the GPU can dereference (HBM, or
+ * pinned host memory when device == NVDSA_HOST_MAPPED_DEVICE). */
+typedef struct nvdsa_tensor {
+  void* data;
+  int32_t dtype;      /* nvdsa_dtype */
+  int32_t ndim;       /* 0..4 */
+  int64_t shape[4];
+  int32_t contiguous; /* 1 when row-major dense */
+  int32_t device;     /* device ordinal, or NVDSA_HOST_MAPPED_DEVICE */
+} nvdsa_tensor;
+
+/* Message of the last failing call on this thread ("" when none). */
+const char* nvdsa_last_error(void);
+
+/* Library version string. */
+const char* nvdsa_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* LightningIndexer top-2048 + HBM slot management, one query per request.
+ * Replaces torch.ops.nanovllm_dsa.fused_li_manage
+ * (reference: csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:646-651,
+ *  checks: ops/fused_li_manage/fused_li_manage_torch_adpt.h:18-92). */
+size_t nvdsa_fused_li_manage_workspace_size(int64_t batch,
+                                            int64_t source_capacity,
+                                            int64_t index_heads);
+
+int nvdsa_fused_li_manage(const nvdsa_tensor* query,
+                          const nvdsa_tensor* index_weights,
+                          const nvdsa_tensor* index_key_cache,
+                          const nvdsa_tensor* index_block_table,
+                          const nvdsa_tensor* num_candidate_tokens,
+                          const nvdsa_tensor* num_cache_tokens,
+                          const nvdsa_tensor* req_pool_entries,
+                          const nvdsa_tensor* cache_slots_pool,
+                          const nvdsa_tensor* topk_src_ids,
+                          const nvdsa_tensor* topk_dst_slots,
+                          const nvdsa_tensor* miss_counts,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Four-query (MTP3) variant: union of four top-2048 sets.
+ * Replaces torch.ops.nanovllm_dsa.fused_li_manage_mtp
+ * (reference: bindings/nanovllm_ops.cpp:652-658,
+ *  checks: ops/fused_li_manage_mtp/fused_li_manage_mtp_torch_adpt.h:20-111). */
+size_t nvdsa_fused_li_manage_mtp_workspace_size(int64_t batch,
+                                                int64_t source_capacity,
+                                                int64_t index_heads);
+
+int nvdsa_fused_li_manage_mtp(const nvdsa_tensor* query,
+                              const nvdsa_tensor* index_weights,
+                              const nvdsa_tensor* index_key_cache,
+                              const nvdsa_tensor* index_block_table,
+                              const nvdsa_tensor* num_candidate_tokens,
+                              const nvdsa_tensor* num_cache_tokens,
+                              const nvdsa_tensor* req_pool_entries,
+                              const nvdsa_tensor* cache_slots_pool,
+                              const nvdsa_tensor* topk_src_ids,
+                              const nvdsa_tensor* topk_dst_slots,
+                              const nvdsa_tensor* miss_src_ids,
+                              const nvdsa_tensor* miss_dst_slots,
+                              const nvdsa_tensor* miss_counts,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* DRAM -> HBM copy of CKV (512) / KPE (64) rows by (src_id, dst_slot) pairs.
+ * Replaces torch.ops.nanovllm_dsa.scatter_copy
+ * (reference: bindings/nanovllm_ops.cpp:659-663,
+ *  checks: ops/kvcache_scatter_copy/kvcache_scatter_copy_torch_adpt.h:16-66). */
+int nvdsa_scatter_copy(const nvdsa_tensor* src_ids,
+                       const nvdsa_tensor* dst_slots,
+                       const nvdsa_tensor* copy_counts,
+                       const nvdsa_tensor* hbm_block_table,
+                       const nvdsa_tensor* dram_block_table,
+                       const nvdsa_tensor* hbm_k_rope,
+                       const nvdsa_tensor* hbm_kv_cache,
+                       const nvdsa_tensor* dram_k_rope,
+                       const nvdsa_tensor* dram_kv_cache,
+                       void* stream);
+
+/* Absorbed-MLA decode attention over top-2048 slots + dense tail.
+ * Replaces torch.ops.nanovllm_dsa.sparse_tail_attention
+ * (reference: bindings/nanovllm_ops.cpp:664-669,
+ *  checks: ops/sparse_tail_attention/sparse_tail_attention_torch_adpt.h:17-88). */
+size_t nvdsa_sparse_tail_attention_workspace_size(int64_t query_rows,
+                                                  int64_t heads,
+                                                  int64_t max_kv_tokens);
+
+int nvdsa_sparse_tail_attention(const nvdsa_tensor* query_rope,
+                                const nvdsa_tensor* query,
+                                const nvdsa_tensor* actual_seq_lengths_query,
+                                const nvdsa_tensor* actual_seq_lengths_kv,
+                                const nvdsa_tensor* num_cache_tokens,
+                                const nvdsa_tensor* topk_dst_slots,
+                                const nvdsa_tensor* hbm_block_table,
+                                const nvdsa_tensor* hbm_k_rope,
+                                const nvdsa_tensor* hbm_kv_cache,
+                                double scale_value,
+                                const nvdsa_tensor* attention_out,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/* MTP3 variant: row 4b+q sees kv_len[b] - (3 - q) tokens.
+ * Replaces torch.ops.nanovllm_dsa.sparse_tail_attention_mtp
+ * (reference: bindings/nanovllm_ops.cpp:670-675,
+ *  checks: ops/sparse_tail_attention_mtp/sparse_tail_attention_mtp_torch_adpt.h:18-96). */
+int nvdsa_sparse_tail_attention_mtp(const nvdsa_tensor* query_rope,
+                                    const nvdsa_tensor* query,
+                                    const nvdsa_tensor* actual_seq_lengths_query,
+                                    const nvdsa_tensor* actual_seq_lengths_kv,
+                                    const nvdsa_tensor* num_cache_tokens,
+                                    const nvdsa_tensor* topk_dst_slots,
+                                    const nvdsa_tensor* hbm_block_table,
+                                    const nvdsa_tensor* hbm_k_rope,
+                                    const nvdsa_tensor* hbm_kv_cache,
+                                    double scale_value,
+                                    const nvdsa_tensor* attention_out,
+                                    void* workspace, size_t workspace_bytes,
+                                    void* stream);
+
+/* Copy of the LIM misses fused with sparse-tail attention.
+ * Replaces torch.ops.nanovllm_dsa.fused_copy_sfa
+ * (reference: bindings/nanovllm_ops.cpp:676-684,
+ *  checks: ops/fused_copy_sfa/fused_copy_sfa_torch_adpt.h:7-110). */
+int nvdsa_fused_copy_sfa(const nvdsa_tensor* query_rope,
+                         const nvdsa_tensor* query,
+                         const nvdsa_tensor* actual_seq_lengths_query,
+                         const nvdsa_tensor* actual_seq_lengths_kv,
+                         const nvdsa_tensor* num_cache_tokens,
+                         const nvdsa_tensor* topk_dst_slots,
+                         const nvdsa_tensor* topk_src_ids,
+                         const nvdsa_tensor* miss_counts,
+                         const nvdsa_tensor* hbm_block_table,
+                         const nvdsa_tensor* dram_block_table,
+                         const nvdsa_tensor* hbm_k_rope,
+                         const nvdsa_tensor* hbm_kv_cache,
+                         const nvdsa_tensor* dram_k_rope,
+                         const nvdsa_tensor* dram_kv_cache,
+                         double scale_value,
+                         const nvdsa_tensor* attention_out,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* MTP3 copy of the union misses fused with MTP3 sparse-tail attention.
+ * Replaces torch.ops.nanovllm_dsa.fused_copy_sfa_mtp
+ * (reference: bindings/nanovllm_ops.cpp:685-694,
+ *  checks: ops/fused_copy_sfa_mtp/fused_copy_sfa_mtp_torch_adpt.h:9-150). */
+int nvdsa_fused_copy_sfa_mtp(const nvdsa_tensor* query_rope,
+                             const nvdsa_tensor* query,
+                             const nvdsa_tensor* actual_seq_lengths_query,
+                             const nvdsa_tensor* actual_seq_lengths_kv,
+                             const nvdsa_tensor* num_cache_tokens,
+                             const nvdsa_tensor* topk_dst_slots,
+                             const nvdsa_tensor* topk_src_ids,
+                             const nvdsa_tensor* miss_src_ids,
+                             const nvdsa_tensor* miss_dst_slots,
+                             const nvdsa_tensor* miss_counts,
+                             const nvdsa_tensor* hbm_block_table,
+                             const nvdsa_tensor* dram_block_table,
+                             const nvdsa_tensor* hbm_k_rope,
+                             const nvdsa_tensor* hbm_kv_cache,
+                             const nvdsa_tensor* dram_k_rope,
+                             const nvdsa_tensor* dram_kv_cache,
+                             double scale_value,
+                             const nvdsa_tensor* attention_out,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Pinned, device-mapped host memory for the DRAM KV caches: the counterpart
+ * of torch_npu.empty_with_swapped_memory (reference
+ * nanovllm/engine/model_runner.py:651-652, ut_ops/test_scatter_copy.py:64-72).
+ * `*host_ptr` is the CPU address; `*device_ptr` the address kernels use. */
+int nvdsa_host_mapped_alloc(size_t bytes, void** host_ptr, void** device_ptr);
+int nvdsa_host_mapped_free(void* host_ptr);
+
+/* ---------------------------------------------------------------------- */
+/* Kernel-level timing (instrumentation; no counterpart in the reference,
+ * whose ut_ops scripts time whole operators with NPU events).  Between
+ * nvdsa_profile_begin and nvdsa_profile_end on one host thread, every kernel
+ * the entry points launch is bracketed by two hipEventRecord calls on its
+ * stream (up to `capacity` launches).  nvdsa_profile_end waits for those
+ * events and writes each launch's duration in milliseconds and its kernel id
+ * (see nvdsa_kernel_name); *recorded receives the number of launches. */
+int nvdsa_profile_begin(int32_t capacity);
+int nvdsa_profile_end(float* durations_ms, int32_t* kernel_ids, int32_t capacity, int32_t* recorded);
+const char* nvdsa_kernel_name(int32_t kernel_id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVDSA_H */

@@ -1,0 +1,123 @@
+// Shared constants and device helpers of the gfx950 DSA offload kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nvdsa {
+
+// Shapes fixed by the operator contracts (reference README_ops.md:19-151,
+// nanovllm/config.py:449-478).
+constexpr int kBlock = 128;          // tokens per KV / index block
+constexpr int kBlockShift = 7;
+constexpr int kTopK = 2048;          // sparse selection width
+constexpr int kCkvDim = 512;         // latent (nope) width
+constexpr int kKpeDim = 64;          // rope width
+constexpr int kQkDim = kCkvDim + kKpeDim;
+constexpr int kIndexDim = 128;       // index head dim
+constexpr int kMtpQueries = 4;       // MTP3 query rows per request
+constexpr int kUnionCap = kTopK * kMtpQueries;
+// Largest usable cache budget C: the reference packs HBM slots into a 14-bit
+// payload field whose all-ones value marks "not cached"
+// (ops/fused_li_manage/op_kernel/fused_li_manage_vector.h:53).
+constexpr int kMaxCacheTokens = (1 << 14) - 1;
+// Largest MTP0 source length (ops/fused_li_manage/op_kernel/fused_li_manage_common.h:52-53).
+constexpr int kMaxSourceCapacity = 1 << 21;
+constexpr int kMaxActualSeqLen = kMaxSourceCapacity - 1;
+
+constexpr int kWave = 64;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+// Element type tags: storage is 16-bit either way; MFMA flavour differs.
+struct Bf16 {
+  using vec8 = bf16x8_t;
+  __device__ static inline float to_float(uint16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+  }
+  // Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+  __device__ static inline uint16_t from_float(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+  }
+  __device__ static inline f32x16_t mfma32(vec8 a, vec8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline f32x4_t mfma16(vec8 a, vec8 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  using vec8 = f16x8_t;
+  __device__ static inline float to_float(uint16_t v) {
+    _Float16 h = __builtin_bit_cast(_Float16, v);
+    return static_cast<float>(h);
+  }
+  __device__ static inline uint16_t from_float(float f) {
+    _Float16 h = static_cast<_Float16>(f);
+    return __builtin_bit_cast(uint16_t, h);
+  }
+  __device__ static inline f32x16_t mfma32(vec8 a, vec8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline f32x4_t mfma16(vec8 a, vec8 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Order-preserving map fp32 -> uint32 (larger float => larger key).
+__device__ inline uint32_t float_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Block-wide exclusive prefix sum of one int per thread (blockDim <= 1024,
+// multiple of 64).  `scratch` must hold blockDim/64 + 1 ints.  Returns the
+// exclusive prefix; *total receives the block sum.  Contains __syncthreads.
+__device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  // inclusive wave scan via shuffles
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) scratch[wid] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < nw; ++w) {
+      int t = scratch[w];
+      scratch[w] = run;
+      run += t;
+    }
+    scratch[nw] = run;
+  }
+  __syncthreads();
+  int excl = scratch[wid] + x - v;
+  *total = scratch[nw];
+  __syncthreads();
+  return excl;
+}
+
+// Exclusive prefix of a 0/1 flag within the wave using a ballot.
+__device__ inline int wave_flag_prefix(bool flag, uint64_t* ballot_out) {
+  const uint64_t b = __ballot(flag);
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = lane == 0 ? 0ull : (b & ((~0ull) >> (64 - lane)));
+  *ballot_out = b;
+  return __popcll(below);
+}
+
+}  // namespace nvdsa

@@ -1,0 +1,113 @@
+// Host-side launch interface between the C ABI layer (nvdsa_abi.hip) and the
+// kernel translation units.  Arguments are already validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace nvdsa {
+
+enum class Elem { kBf16, kF16 };
+
+// Kernel ids of the timing instrumentation (nvdsa_profile_*).
+enum KernelId : int {
+  kKernScatter = 0,
+  kKernLimScore = 1,
+  kKernLimManage = 2,
+  kKernLimManageMtp = 3,
+  kKernSfaSplit = 4,
+  kKernSfaSplitFused = 5,
+  kKernSfaCombine = 6,
+  kKernCount = 7
+};
+// Bracket one kernel launch with timing events when instrumentation is on
+// for the calling thread (no-ops otherwise).
+void prof_before(hipStream_t stream, int kernel_id);
+void prof_after(hipStream_t stream);
+
+// ---- scatter_copy --------------------------------------------------------
+struct ScatterArgs {
+  const int32_t* src_ids;      // [B, cap]
+  const int32_t* dst_slots;    // [B, cap]
+  const int32_t* copy_counts;  // [B]
+  const int32_t* hbm_table;    // [B, hbm_cols]
+  const int32_t* dram_table;   // [B, dram_cols]
+  void* hbm_kpe;               // [hbm_blocks, 128, 64]
+  void* hbm_ckv;               // [hbm_blocks, 128, 512]
+  const void* dram_kpe;        // [dram_blocks, 128, 64]
+  const void* dram_ckv;        // [dram_blocks, 128, 512]
+  int64_t batch;
+  int64_t cap;
+  int64_t hbm_cols;
+  int64_t dram_cols;
+  int64_t hbm_blocks;
+  int64_t dram_blocks;
+};
+hipError_t launch_scatter_copy(const ScatterArgs& a, hipStream_t stream);
+
+// ---- fused_li_manage (MTP0 and MTP3) ---------------------------------------
+struct LimArgs {
+  const void* query;            // [B*Q, H, 128]
+  const void* weights;          // [B*Q, H]
+  const void* key_cache;        // [key_blocks, 128, 1, 128]
+  const int32_t* block_table;   // [B, cols]
+  const int32_t* num_candidates;  // [B]
+  const int32_t* num_cache;     // [B]
+  const int32_t* pool_entries;  // [B]
+  int32_t* pool;                // [pool_rows, cols*128]
+  int32_t* topk_src;            // [B*Q, 1, 2048]
+  int32_t* topk_dst;            // [B*Q, 1, 2048]
+  int32_t* miss_src;            // [B, 8192]   (MTP only)
+  int32_t* miss_dst;            // [B, 8192]   (MTP only)
+  int32_t* miss_counts;         // [B]
+  int64_t batch;
+  int64_t heads;
+  int64_t cols;                 // block-table columns
+  int64_t key_blocks;
+  int64_t pool_rows;
+  int64_t source_capacity;      // cols * 128
+  Elem elem;
+  void* workspace;
+  size_t workspace_bytes;
+};
+size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries);
+hipError_t launch_fused_li_manage(const LimArgs& a, hipStream_t stream);
+hipError_t launch_fused_li_manage_mtp(const LimArgs& a, hipStream_t stream);
+
+// ---- sparse-tail attention (+ fused copy) --------------------------------
+struct SfaArgs {
+  const void* query_rope;       // [R, N, 64]
+  const void* query;            // [R, N, 512]
+  const int32_t* seq_kv;        // [B]
+  const int32_t* num_cache;     // [B]
+  const int32_t* topk_dst;      // [R, 1, 2048]
+  const int32_t* hbm_table;     // [B, hbm_cols]
+  void* hbm_kpe;                // [hbm_blocks, 128, 1, 64]
+  void* hbm_ckv;                // [hbm_blocks, 128, 1, 512]
+  void* out;                    // [R, N, 512]
+  int64_t batch;
+  int64_t rows_per_request;     // 1 or 4
+  int64_t heads;
+  int64_t hbm_cols;
+  int64_t hbm_blocks;
+  float scale;
+  Elem elem;
+  // fused copy (null when not fused)
+  const int32_t* copy_src;      // MTP0: topk_src_ids [B, 2048]; MTP3: miss_src_ids [B, 8192]
+  const int32_t* copy_dst;      // MTP0: topk_dst_slots; MTP3: miss_dst_slots
+  const int32_t* copy_counts;   // [B]
+  int64_t copy_cap;             // 2048 or 8192
+  const int32_t* dram_table;    // [B, dram_cols]
+  const void* dram_kpe;
+  const void* dram_ckv;
+  int64_t dram_cols;
+  int64_t dram_blocks;
+  void* workspace;
+  size_t workspace_bytes;
+};
+size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens);
+hipError_t launch_sparse_tail_attention(const SfaArgs& a, hipStream_t stream);
+hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream);
+
+}  // namespace nvdsa

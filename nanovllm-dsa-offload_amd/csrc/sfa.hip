@@ -1,0 +1,408 @@
+// sparse_tail_attention(_mtp) and fused_copy_sfa(_mtp): absorbed-MLA decode
+// attention over the 2048 selected HBM slots plus the dense tail.
+//
+// Row rules (ops/sparse_tail_attention/op_kernel/nanovllm_sparse_tail_attention_kernel_mla.h:325-353):
+//   L  = kv_len[b] - (MTP3 ? 3 - q : 0)       visible length of query row (b, q)
+//   C == 0            -> keys = slots [0, L)
+//   2048 <= C <= L    -> keys = topk_dst_slots[row, 0:2048] ++ slots [C, L)
+//   otherwise         -> output zeros
+// A key is used only when 0 <= slot < L and its block-table entry resolves
+// (the s2IdLimit bound of nanovllm_sparse_tail_attention_service_vector_mla.h:792-797).
+//   o = softmax(scale * (q . ckv + q_rope . kpe)) . ckv     fp32 accumulate, 16-bit store.
+//
+// Kernel design (split-KV flash decode):
+//   grid = rows x splits x ceil(heads/64); a 256-thread workgroup owns one
+//   row, one split of its key list and 64 heads (one 16-head MFMA tile per
+//   wavefront).  Keys are processed in tiles of 32; split s takes tiles
+//   s, s+S, s+2S, ... so host-sourced miss rows (a prefix of the list) spread
+//   over all splits.  Each tile is gathered once into LDS in two layouts:
+//   row-major [key][576] for S^T = K . Q^T (v_mfma_f32_16x16x32, A = keys,
+//   B = the wave's queries held in registers) and transposed [512][key] for
+//   O^T = V^T . P^T, whose B operand is the softmax numerator already sitting
+//   in the S^T accumulator lanes.  Online softmax in base 2; a second kernel
+//   merges the per-split (max, sum, numerator) partials.
+//   fused_copy_sfa: tiles holding misses read those rows from host-mapped
+//   DRAM, use them for attention and store them to their HBM slots.
+#include <cfloat>
+
+#include "nvdsa_common.h"
+#include "nvdsa_kernels.h"
+#include "row_copy.h"
+
+namespace nvdsa {
+namespace {
+
+constexpr int kTileKeys = 32;
+constexpr int kAttnThreads = 256;
+constexpr int kHeadsPerBlock = 64;
+constexpr int kKStride = kQkDim + 8;       // LDS row of the key tile (elements)
+constexpr int kVStride = kTileKeys + 8;    // LDS row of the transposed value tile
+constexpr int kChunksPerKey = kQkDim * 2 / 16;  // 72 x 16 bytes
+constexpr int kMaxSplits = 16;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct RowPlan {
+  int active;      // 1 when the row attends
+  int sparse;      // number of sparse list entries (0 or 2048)
+  int tail_start;  // first tail slot
+  int count;       // total key list length
+  int lvis;        // visible length L
+};
+
+__device__ inline RowPlan plan_row(const SfaArgs& a, int64_t row) {
+  const int64_t b = row / a.rows_per_request;
+  const int q = static_cast<int>(row - b * a.rows_per_request);
+  int64_t lvis = a.seq_kv[b];
+  if (a.rows_per_request > 1) {
+    const int hidden = static_cast<int>(a.rows_per_request) - 1 - q;
+    lvis = lvis > hidden ? lvis - hidden : 0;
+  }
+  if (lvis < 0) lvis = 0;
+  const int c = a.num_cache[b];
+  RowPlan p{0, 0, 0, 0, static_cast<int>(lvis > INT32_MAX ? INT32_MAX : lvis)};
+  if (c == 0) {
+    p.active = lvis > 0;
+    p.tail_start = 0;
+    p.count = p.lvis;
+  } else if (c >= kTopK && static_cast<int64_t>(c) <= lvis) {
+    p.active = 1;
+    p.sparse = kTopK;
+    p.tail_start = c;
+    p.count = kTopK + (p.lvis - c);
+  }
+  return p;
+}
+
+struct Partials {
+  float* o;   // [R][S][H][512]
+  float* ml;  // [R][S][H][2]
+};
+
+Partials carve(void* ws, int64_t rows, int64_t splits, int64_t heads) {
+  Partials p;
+  p.o = static_cast<float*>(ws);
+  p.ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(sizeof(float) * rows * splits * heads * kCkvDim));
+  return p;
+}
+
+int choose_splits(int64_t rows, int64_t head_groups) {
+  if (rows <= 0 || head_groups <= 0) return 1;
+  // Aim at ~2 resident workgroups per CU on 256 CUs.
+  const int64_t target = 512;
+  int64_t s = ceil_div(target, rows * head_groups);
+  if (s < 1) s = 1;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return static_cast<int>(s);
+}
+
+template <typename T, bool FUSED>
+__global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Partials part, int splits) {
+  __shared__ uint16_t ks[kTileKeys * kKStride];
+  __shared__ uint16_t vt[kCkvDim * kVStride];
+  __shared__ int64_t key_src[kTileKeys];   // source row (HBM or DRAM), -1 = masked
+  __shared__ int64_t key_dst[kTileKeys];   // HBM row a DRAM-sourced key is stored to, -1 = none
+  __shared__ int key_kind[kTileKeys];      // 0 masked, 1 HBM, 2 DRAM
+  __shared__ int key_use[kTileKeys];       // 1 when the key enters the softmax
+
+  const int64_t row = blockIdx.x / splits;
+  const int split = static_cast<int>(blockIdx.x - row * splits);
+  const int hg = blockIdx.y;
+  const int64_t b = row / a.rows_per_request;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int h0 = hg * kHeadsPerBlock + wave * 16;
+  const bool wave_active = h0 < a.heads;
+  const int head = h0 + l16;
+  const int64_t H = a.heads;
+
+  const RowPlan plan = plan_row(a, row);
+  // Copy work (fused): MTP0 copies pairs j < miss_counts[b] of the row's own list.
+  int copy_count = 0;
+  if (FUSED) {
+    copy_count = a.copy_counts[b];
+    copy_count = copy_count < 0 ? 0 : (copy_count > kTopK ? kTopK : copy_count);
+  }
+  const int list_len = plan.active ? plan.count : (FUSED ? copy_count : 0);
+  const int ntiles = static_cast<int>(ceil_div(list_len, kTileKeys));
+
+  // Query fragments for this wave: lane holds q[head][32*kk + 8*g .. +8].
+  uint4 qf[kQkDim / 32];
+  {
+    const uint4* qn = static_cast<const uint4*>(a.query) + (row * H + head) * (kCkvDim / 8);
+    const uint4* qr = static_cast<const uint4*>(a.query_rope) + (row * H + head) * (kKpeDim / 8);
+    const bool hv = wave_active && head < a.heads && plan.active;
+#pragma unroll
+    for (int kk = 0; kk < kQkDim / 32; ++kk) {
+      const int chunk = kk * 4 + g;  // 16-byte chunk index within the 576-dim row
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (hv) v = chunk < kCkvDim / 8 ? qn[chunk] : qr[chunk - kCkvDim / 8];
+      qf[kk] = v;
+    }
+  }
+  const float qscale = a.scale * kLog2e;
+  float m_run = -INFINITY;  // running max (base-2 logits) of head `head`
+  float l_run = 0.f;        // this lane's share of the running sum
+  f32x4_t oacc[kCkvDim / 16];
+#pragma unroll
+  for (int i = 0; i < kCkvDim / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int32_t* topk = a.topk_dst + row * kTopK;
+  const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
+
+  for (int tile = split; tile < ntiles; tile += splits) {
+    const int kbase = tile * kTileKeys;
+    if (tid < kTileKeys) {
+      const int j = kbase + tid;
+      int kind = 0, use = 0;
+      int64_t src = -1, dst = -1;
+      if (j < list_len) {
+        int slot;
+        if (plan.active) {
+          slot = j < plan.sparse ? topk[j] : plan.tail_start + (j - plan.sparse);
+        } else {
+          slot = a.copy_dst[b * a.copy_cap + j];
+        }
+        int64_t hrow = -1;
+        if (slot >= 0 && (slot >> kBlockShift) < a.hbm_cols) {
+          const int32_t blk = hbm_row_table[slot >> kBlockShift];
+          if (blk >= 0 && blk < a.hbm_blocks) hrow = static_cast<int64_t>(blk) * kBlock + (slot & (kBlock - 1));
+        }
+        use = plan.active && hrow >= 0 && slot < plan.lvis;
+        if (use) {
+          kind = 1;
+          src = hrow;
+        }
+        if (FUSED && j < copy_count) {
+          const RowAddr ra =
+              resolve_pair(a.copy_src[b * a.copy_cap + j], a.copy_dst[b * a.copy_cap + j],
+                           a.dram_table + b * a.dram_cols, a.dram_cols, a.dram_blocks, hbm_row_table, a.hbm_cols,
+                           a.hbm_blocks);
+          if (ra.src_row >= 0) {
+            kind = 2;
+            src = ra.src_row;
+            dst = ra.dst_row;
+          }
+        }
+      }
+      key_kind[tid] = kind;
+      key_src[tid] = src;
+      key_dst[tid] = dst;
+      key_use[tid] = use;
+    }
+    __syncthreads();
+    // Gather the tile: 32 keys x 72 chunks of 16 bytes.
+    for (int cidx = tid; cidx < kTileKeys * kChunksPerKey; cidx += kAttnThreads) {
+      const int k = cidx / kChunksPerKey;
+      const int part_i = cidx - k * kChunksPerKey;
+      const int kind = key_kind[k];
+      const int64_t src = key_src[k];
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (kind == 1) {
+        v = part_i < 64 ? static_cast<const uint4*>(a.hbm_ckv)[src * 64 + part_i]
+                        : static_cast<const uint4*>(a.hbm_kpe)[src * 8 + (part_i - 64)];
+      } else if (FUSED && kind == 2) {
+        v = part_i < 64 ? static_cast<const uint4*>(a.dram_ckv)[src * 64 + part_i]
+                        : static_cast<const uint4*>(a.dram_kpe)[src * 8 + (part_i - 64)];
+        const int64_t dst = key_dst[k];
+        if (part_i < 64)
+          static_cast<uint4*>(a.hbm_ckv)[dst * 64 + part_i] = v;
+        else
+          static_cast<uint4*>(a.hbm_kpe)[dst * 8 + (part_i - 64)] = v;
+      }
+      *reinterpret_cast<uint4*>(&ks[k * kKStride + part_i * 8]) = v;
+      if (part_i < 64) {
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) vt[(part_i * 8 + x) * kVStride + k] = e[x];
+      }
+    }
+    __syncthreads();
+
+    if (wave_active && plan.active) {
+      // S^T tile: two 16-key blocks; lane holds S[head][kt*16 + 4g + i].
+      f32x4_t sacc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        const uint16_t* krow = &ks[(kt * 16 + l16) * kKStride + g * 8];
+#pragma unroll
+        for (int kk = 0; kk < kQkDim / 32; ++kk) {
+          const uint4 kf = *reinterpret_cast<const uint4*>(krow + kk * 32);
+          acc = T::mfma16(__builtin_bit_cast(typename T::vec8, kf), __builtin_bit_cast(typename T::vec8, qf[kk]),
+                          acc);
+        }
+        sacc[kt] = acc;
+      }
+      float sv[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int k = kt * 16 + 4 * g + i;
+          const float x = key_use[k] ? sacc[kt][i] * qscale : -INFINITY;
+          sv[kt * 4 + i] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      if (m_new != -INFINITY) {
+        const float alpha = exp2f(m_run - m_new);  // m_run == -inf gives 0
+        m_run = m_new;
+        float psum = 0.f;
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          p[i] = exp2f(sv[i] - m_new);
+          psum += p[i];
+        }
+        l_run = l_run * alpha + psum;
+        // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
+        // ~16 mantissa bits of P instead of 8.
+        typename T::vec8 pb_hi, pb_lo;
+        uint16_t* phs = reinterpret_cast<uint16_t*>(&pb_hi);
+        uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          phs[i] = T::from_float(p[i]);
+          pls[i] = T::from_float(p[i] - T::to_float(phs[i]));
+        }
+#pragma unroll
+        for (int dt = 0; dt < kCkvDim / 16; ++dt) {
+          const uint16_t* vrow = &vt[(dt * 16 + l16) * kVStride];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * g);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * g);
+          const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          f32x4_t acc = oacc[dt];
+          acc[0] *= alpha;
+          acc[1] *= alpha;
+          acc[2] *= alpha;
+          acc[3] *= alpha;
+          acc = T::mfma16(af, pb_hi, acc);
+          oacc[dt] = T::mfma16(af, pb_lo, acc);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Split partials: max, sum and un-normalised numerator per head.
+  if (!wave_active || head >= a.heads) return;
+  float lsum = l_run + __shfl_xor(l_run, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  const int64_t pidx = (row * splits + split) * H + head;
+  if (g == 0) {
+    part.ml[pidx * 2 + 0] = m_run;
+    part.ml[pidx * 2 + 1] = lsum;
+  }
+  if (lsum > 0.f) {
+    float* od = part.o + pidx * kCkvDim;
+#pragma unroll
+    for (int dt = 0; dt < kCkvDim / 16; ++dt)
+      *reinterpret_cast<float4*>(od + dt * 16 + 4 * g) =
+          make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
+  }
+}
+
+// Merge split partials: one 128-thread workgroup per (row, head), 4 dims per thread.
+template <typename T>
+__global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
+  const int64_t row = blockIdx.x;
+  const int head = blockIdx.y;
+  const int64_t H = a.heads;
+  float mmax = -INFINITY;
+  for (int s = 0; s < splits; ++s) {
+    const int64_t pidx = (row * splits + s) * H + head;
+    if (part.ml[pidx * 2 + 1] > 0.f) mmax = fmaxf(mmax, part.ml[pidx * 2]);
+  }
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float total = 0.f;
+  if (mmax != -INFINITY) {
+    for (int s = 0; s < splits; ++s) {
+      const int64_t pidx = (row * splits + s) * H + head;
+      const float l = part.ml[pidx * 2 + 1];
+      if (!(l > 0.f)) continue;
+      const float w = exp2f(part.ml[pidx * 2] - mmax);
+      total += l * w;
+      const float4 o = reinterpret_cast<const float4*>(part.o + pidx * kCkvDim)[threadIdx.x];
+      acc.x += o.x * w;
+      acc.y += o.y * w;
+      acc.z += o.z * w;
+      acc.w += o.w * w;
+    }
+  }
+  const float inv = total > 0.f ? 1.f / total : 0.f;
+  uint16_t* out = static_cast<uint16_t*>(a.out) + (row * H + head) * kCkvDim + threadIdx.x * 4;
+  const uint32_t lo = static_cast<uint32_t>(T::from_float(acc.x * inv)) |
+                      (static_cast<uint32_t>(T::from_float(acc.y * inv)) << 16);
+  const uint32_t hi = static_cast<uint32_t>(T::from_float(acc.z * inv)) |
+                      (static_cast<uint32_t>(T::from_float(acc.w * inv)) << 16);
+  *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
+}
+
+template <typename T, bool FUSED>
+hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
+  const int64_t rows = a.batch * a.rows_per_request;
+  if (rows == 0) return hipSuccess;
+  const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
+  const int splits = choose_splits(rows, hgroups);
+  const Partials p = carve(a.workspace, rows, splits, a.heads);
+  prof_before(stream, FUSED ? kKernSfaSplitFused : kKernSfaSplit);
+  hipLaunchKernelGGL((sfa_split_kernel<T, FUSED>), dim3(static_cast<uint32_t>(rows * splits), hgroups),
+                     dim3(kAttnThreads), 0, stream, a, p, splits);
+  prof_after(stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  prof_before(stream, kKernSfaCombine);
+  hipLaunchKernelGGL((sfa_combine_kernel<T>), dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads)),
+                     dim3(128), 0, stream, a, p, splits);
+  prof_after(stream);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens) {
+  (void)max_kv_tokens;
+  const int64_t splits = choose_splits(query_rows, ceil_div(heads, kHeadsPerBlock));
+  return align256(sizeof(float) * query_rows * splits * heads * kCkvDim) +
+         align256(sizeof(float) * query_rows * splits * heads * 2);
+}
+
+hipError_t launch_sparse_tail_attention(const SfaArgs& a, hipStream_t stream) {
+  return a.elem == Elem::kBf16 ? launch_sfa<Bf16, false>(a, stream) : launch_sfa<F16, false>(a, stream);
+}
+
+hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream) {
+  if (a.rows_per_request > 1) {
+    // MTP3: copy the compact union misses, then attend; both on `stream`.
+    ScatterArgs s{};
+    s.src_ids = a.copy_src;
+    s.dst_slots = a.copy_dst;
+    s.copy_counts = a.copy_counts;
+    s.hbm_table = a.hbm_table;
+    s.dram_table = a.dram_table;
+    s.hbm_kpe = a.hbm_kpe;
+    s.hbm_ckv = a.hbm_ckv;
+    s.dram_kpe = a.dram_kpe;
+    s.dram_ckv = a.dram_ckv;
+    s.batch = a.batch;
+    s.cap = a.copy_cap;
+    s.hbm_cols = a.hbm_cols;
+    s.dram_cols = a.dram_cols;
+    s.hbm_blocks = a.hbm_blocks;
+    s.dram_blocks = a.dram_blocks;
+    hipError_t e = launch_scatter_copy(s, stream);
+    if (e != hipSuccess) return e;
+    return launch_sparse_tail_attention(a, stream);
+  }
+  return a.elem == Elem::kBf16 ? launch_sfa<Bf16, true>(a, stream) : launch_sfa<F16, true>(a, stream);
+}
+
+}  // namespace nvdsa

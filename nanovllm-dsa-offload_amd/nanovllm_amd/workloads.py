@@ -1,0 +1,355 @@
+"""Seeded synthetic workloads for the DSA offload chain.
+
+Builds the inputs of one target layer's stable decode step the way the
+reference's op tests and perf scripts do (ut_ops/test_fused_li_manage_scatter.py,
+ut_ops/test_fused_copy_sfa.py, ut_ops/test_fused_li_manage_perf.py:221-257):
+paged bf16 index keys and latent KV with random block tables, an index query
+with U(0,1) head weights, a persistent slot pool holding a previous
+selection (so that 5-15% of this step's top-2048 miss), an HBM cache
+consistent with that pool, DRAM caches in host-mapped memory, and the
+attention query.
+
+``guard=True`` makes the integer outputs well defined under any fp32
+summation order: it computes float64 scores plus a per-token bound on the
+fp32 reduction error, and while the top-2048 boundary (or the victim
+boundary when C > 2048) is closer than the two tokens' bounds it halves the
+index key of the token just outside (or inside) that boundary.  Halving a
+bf16 row is exact and scales that token's score by exactly 1/2 (the score is
+positively homogeneous in the key), so no other token moves.
+
+Everything is generated on the CPU as torch tensors; ``to_device`` moves a
+case to the GPU.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+BLOCK = 128
+TOPK = 2048
+CKV = 512
+KPE = 64
+IDX = 128
+MTP_Q = 4
+
+_ERR_UNIT = 2.0 ** -24 * 256  # fp32 reduction-order error per unit of sum |terms|
+
+
+def _bf16(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return x.to(dtype)
+
+
+def _f64(t: torch.Tensor) -> np.ndarray:
+    return t.to(torch.float64).numpy()
+
+
+@dataclass
+class ChainCase:
+    """Inputs (and shapes) of one LIM -> copy -> SFA layer step."""
+
+    tensors: dict[str, torch.Tensor] = field(default_factory=dict)
+    meta: dict = field(default_factory=dict)
+
+    def __getitem__(self, key):
+        return self.tensors[key]
+
+    def to_device(self, device, host_mapped: bool = True) -> "ChainCase":
+        """Copy to ``device``; DRAM caches go to host-mapped memory unless
+        ``host_mapped`` is False (then plain HBM)."""
+        out = {}
+        for name, t in self.tensors.items():
+            if name in ("dram_kv_cache", "dram_k_rope") and host_mapped:
+                from .host_memory import host_mapped_pair
+
+                gpu, cpu = host_mapped_pair(t.shape, t.dtype, device)
+                cpu.copy_(t)
+                out[name] = gpu
+                out[name + "_host"] = cpu
+            else:
+                out[name] = t.to(device)
+        return ChainCase(out, dict(self.meta))
+
+
+def _topk_order(scores: np.ndarray) -> np.ndarray:
+    n = scores.shape[0]
+    return np.lexsort((np.arange(n), -scores))
+
+
+def make_chain_case(
+    batch: int,
+    source_lens,
+    cache_tokens,
+    tails,
+    *,
+    index_heads: int = 32,
+    attn_heads: int = 64,
+    miss_frac=(0.05, 0.15),
+    seed: int = 0,
+    dtype: torch.dtype = torch.bfloat16,
+    mtp: bool = False,
+    guard: bool = True,
+    extra_pool_rows: int = 1,
+    query_scale: float = 1.0,
+    structured_scores: bool = False,
+) -> ChainCase:
+    """One layer step.  ``source_lens`` / ``cache_tokens`` / ``tails`` are
+    per-request lists (or scalars); source lengths are whole 128-token
+    blocks.  ``mtp`` builds four index/attention queries per request.
+    ``structured_scores`` uses the reference's closed-form index (score ==
+    token id, ut_ops/test_fused_li_manage.py:146-173)."""
+    B = int(batch)
+    as_list = lambda v: [int(x) for x in (v if hasattr(v, "__len__") else [v] * B)]  # noqa: E731
+    N = as_list(source_lens)
+    C = as_list(cache_tokens)
+    T = as_list(tails)
+    Q = MTP_Q if mtp else 1
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+
+    cols = max(1, math.ceil(max(N) / BLOCK))
+    cap = cols * BLOCK
+    # ---- index keys, paged -------------------------------------------------
+    nblk = [math.ceil(n / BLOCK) for n in N]
+    total_idx = max(1, sum(nblk))
+    perm = torch.randperm(total_idx, generator=g).to(torch.int32)
+    index_table = torch.full((B, cols), -1, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        index_table[b, : nblk[b]] = perm[off : off + nblk[b]]
+        off += nblk[b]
+    if structured_scores:
+        keys = torch.zeros(total_idx, BLOCK, 1, IDX)
+        for b in range(B):
+            ids = torch.arange(nblk[b] * BLOCK)
+            rows = keys[index_table[b, : nblk[b]].long()].view(-1, IDX)
+            rows[:, 0] = (ids % 64).float()
+            rows[:, 1] = ((ids // 64) % 64).float()
+            rows[:, 2] = ((ids // 4096) % 64).float()
+            rows[:, 3] = (ids // 262144).float()
+            keys[index_table[b, : nblk[b]].long()] = rows.view(nblk[b], BLOCK, 1, IDX)
+        key_cache = keys.to(dtype)
+        q_index = torch.zeros(B * Q, index_heads, IDX)
+        q_index[:, 0, 0] = 1.0
+        q_index[:, 0, 1] = 64.0
+        q_index[:, 0, 2] = 4096.0
+        q_index[:, 0, 3] = 262144.0
+        q_index = q_index.to(dtype)
+        weights = torch.zeros(B * Q, index_heads)
+        weights[:, 0] = 1.0
+        weights = weights.to(dtype)
+    else:
+        key_cache = torch.randn(total_idx, BLOCK, 1, IDX, generator=g).to(dtype)
+        q_index = torch.randn(B * Q, index_heads, IDX, generator=g).to(dtype)
+        weights = torch.rand(B * Q, index_heads, generator=g).to(dtype)
+
+    kc = key_cache.view(-1, IDX)  # physical rows
+
+    def rows_of(b: int) -> torch.Tensor:
+        n = N[b]
+        t = torch.arange(n)
+        return index_table[b, t // BLOCK].long() * BLOCK + (t % BLOCK)
+
+    def scores_of(b: int, phys: torch.Tensor):
+        k = _f64(kc[phys])
+        s, e = [], []
+        for q in range(Q):
+            qq = _f64(q_index[b * Q + q])
+            ww = _f64(weights[b * Q + q])
+            dots = k @ qq.T
+            s.append(np.maximum(dots, 0.0) @ ww)
+            e.append(_ERR_UNIT * (np.abs(k) @ np.abs(qq).T) @ np.abs(ww))
+        return np.stack(s), np.stack(e)
+
+    pool_rows = B + extra_pool_rows
+    pool = torch.full((pool_rows, cap), -777, dtype=torch.int32)
+    pool_entries = torch.from_numpy(rng.permutation(pool_rows)[:B].astype(np.int32))
+    miss_target = []
+    halvings = 0
+    cached_lists, slot_lists = [], []
+    for b in range(B):
+        phys = rows_of(b)
+        s, e = scores_of(b, phys)
+        n, c = N[b], C[b]
+        active = n >= TOPK and c >= TOPK and c <= n if not mtp else (n >= TOPK and c > 0 and c >= min(n, 8192) and c <= n)
+        # ---- top-k boundary guard --------------------------------------------
+        if guard and active and not structured_scores:
+            for _ in range(4 * n):
+                changed = False
+                for q in range(Q):
+                    order = _topk_order(s[q])
+                    if n <= TOPK:
+                        continue
+                    a, z = order[TOPK - 1], order[TOPK]
+                    if s[q, a] - s[q, z] < e[q, a] + e[q, z] + 1e-12:
+                        kc[phys[z]] = (kc[phys[z]].float() * 0.5).to(dtype)
+                        s[:, z] *= 0.5
+                        e[:, z] *= 0.5
+                        halvings += 1
+                        changed = True
+                if not changed:
+                    break
+        pool[pool_entries[b]].fill_(-1)
+        if not active:
+            miss_target.append(0)
+            cached_lists.append(np.zeros(0, np.int64))
+            slot_lists.append(np.zeros(0, np.int64))
+            continue
+        sel_rows = [np.sort(_topk_order(s[q])[:TOPK]) for q in range(Q)]
+        if mtp:
+            seen = set()
+            union = []
+            for row in sel_rows:
+                for t in row:
+                    if int(t) not in seen:
+                        seen.add(int(t))
+                        union.append(int(t))
+            union = np.asarray(union, np.int64)
+        else:
+            union = sel_rows[0]
+        frac = rng.uniform(*miss_frac)
+        m = int(round(frac * union.size))
+        m = max(0, min(m, union.size, n - c))
+        miss_target.append(m)
+        misses = rng.choice(union, size=m, replace=False) if m else np.zeros(0, np.int64)
+        in_union = np.zeros(n, bool)
+        in_union[union] = True
+        is_miss = np.zeros(n, bool)
+        is_miss[misses] = True
+        hits = union[~is_miss[union]]
+        need = c - hits.size
+        smax = s.max(axis=0)
+        outside = np.nonzero(~in_union)[0]
+        # fillers: previously selected tokens just outside this step's union
+        outside_rank = outside[np.argsort(-smax[outside], kind="stable")]
+        pool_sz = min(outside_rank.size, max(need, 4 * c))
+        fillers = rng.choice(outside_rank[:pool_sz], size=need, replace=False) if need else np.zeros(0, np.int64)
+        # ---- victim boundary guard (only when the victim set is not forced) --
+        if guard and m > 0 and fillers.size > m and not structured_scores:
+            emax = e.max(axis=0)
+            for _ in range(4 * fillers.size):
+                order = fillers[np.lexsort((fillers, smax[fillers]))]
+                lo, hi = order[m - 1], order[m]
+                if smax[hi] - smax[lo] >= emax[lo] + emax[hi] + 1e-12:
+                    break
+                kc[phys[lo]] = (kc[phys[lo]].float() * 0.5).to(dtype)
+                s[:, lo] *= 0.5
+                e[:, lo] *= 0.5
+                smax[lo] *= 0.5
+                emax[lo] *= 0.5
+                halvings += 1
+        cached = np.concatenate([hits, fillers]).astype(np.int64)
+        slots = rng.permutation(c).astype(np.int64)
+        pool[pool_entries[b], torch.from_numpy(cached)] = torch.from_numpy(slots.astype(np.int32))
+        cached_lists.append(cached)
+        slot_lists.append(slots)
+
+    # ---- latent KV: DRAM (full prompt) and HBM (C slots + tail) ------------------
+    dram_table = torch.full((B, cols), -1, dtype=torch.int32)
+    dperm = torch.randperm(total_idx, generator=g).to(torch.int32)
+    off = 0
+    for b in range(B):
+        dram_table[b, : nblk[b]] = dperm[off : off + nblk[b]]
+        off += nblk[b]
+    dram_ckv = torch.randn(total_idx, BLOCK, CKV, generator=g).to(dtype)
+    dram_kpe = torch.randn(total_idx, BLOCK, KPE, generator=g).to(dtype)
+    hlen = [C[b] + T[b] for b in range(B)]
+    hblk = [max(1, math.ceil(h / BLOCK)) for h in hlen]
+    hcols = max(hblk)
+    total_h = sum(hblk)
+    hperm = torch.randperm(total_h, generator=g).to(torch.int32)
+    hbm_table = torch.full((B, hcols), -1, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        hbm_table[b, : hblk[b]] = hperm[off : off + hblk[b]]
+        off += hblk[b]
+    hbm_ckv = torch.randn(total_h, BLOCK, 1, CKV, generator=g).to(dtype)
+    hbm_kpe = torch.randn(total_h, BLOCK, 1, KPE, generator=g).to(dtype)
+    hc = hbm_ckv.view(-1, CKV)
+    hk = hbm_kpe.view(-1, KPE)
+    dc = dram_ckv.view(-1, CKV)
+    dk = dram_kpe.view(-1, KPE)
+    for b in range(B):
+        cached, slots = cached_lists[b], slot_lists[b]
+        if cached.size == 0:
+            continue
+        st = torch.from_numpy(slots)
+        hrow = hbm_table[b, st // BLOCK].long() * BLOCK + st % BLOCK
+        ct = torch.from_numpy(cached)
+        drow = dram_table[b, ct // BLOCK].long() * BLOCK + ct % BLOCK
+        hc[hrow] = dc[drow]
+        hk[hrow] = dk[drow]
+
+    R = B * Q
+    q_attn = (torch.randn(R, attn_heads, CKV, generator=g) * query_scale).to(dtype)
+    q_rope = (torch.randn(R, attn_heads, KPE, generator=g) * query_scale).to(dtype)
+    tensors = {
+        "query_index": q_index,
+        "index_weights": weights,
+        "index_key_cache": key_cache,
+        "index_block_table": index_table,
+        "num_candidate_tokens": torch.tensor(N, dtype=torch.int32),
+        "num_cache_tokens": torch.tensor(C, dtype=torch.int32),
+        "req_pool_entries": pool_entries,
+        "cache_slots_pool": pool,
+        "query": q_attn,
+        "query_rope": q_rope,
+        "actual_seq_lengths_query": torch.arange(Q, R + 1, Q, dtype=torch.int32)[:B]
+        if Q > 1
+        else torch.arange(1, B + 1, dtype=torch.int32),
+        "actual_seq_lengths_kv": torch.tensor(hlen, dtype=torch.int32),
+        "hbm_block_table": hbm_table,
+        "dram_block_table": dram_table,
+        "hbm_kv_cache": hbm_ckv,
+        "hbm_k_rope": hbm_kpe,
+        "dram_kv_cache": dram_ckv,
+        "dram_k_rope": dram_kpe,
+    }
+    # caller-owned outputs
+    tensors["topk_src_ids"] = torch.full((R, 1, TOPK), -1, dtype=torch.int32)
+    tensors["topk_dst_slots"] = torch.full((R, 1, TOPK), -1, dtype=torch.int32)
+    tensors["miss_counts"] = torch.full((B,), -1, dtype=torch.int32)
+    if mtp:
+        tensors["miss_src_ids"] = torch.full((B, 8192), -1, dtype=torch.int32)
+        tensors["miss_dst_slots"] = torch.full((B, 8192), -1, dtype=torch.int32)
+    tensors["attention_out"] = torch.zeros(R, attn_heads, CKV, dtype=dtype)
+    meta = {
+        "batch": B,
+        "source_lens": N,
+        "cache_tokens": C,
+        "tails": T,
+        "mtp": mtp,
+        "queries": Q,
+        "miss_target": miss_target,
+        "halvings": halvings,
+        "scale": 1.0 / math.sqrt(CKV + KPE),
+        "dtype": dtype,
+    }
+    return ChainCase(tensors, meta)
+
+
+def baseline_config(index: int, seed: int = 0, dtype: torch.dtype = torch.bfloat16, guard: bool = False) -> ChainCase:
+    """The configurations of BASELINE.json ``configs`` (0..3) at full size.
+
+    cfg0: bs=1, 20480-token prompt, tail 37, C=2048.
+    cfg1: bs=24, 32768-token prompts, tails U[1,127], miss 5-15%, C=2048.
+    cfg2: bs=64, prompts U[20K,64K] (whole blocks), C=2048 (fused path).
+    cfg3: MTP3, bs=16 x 4 queries, 48K prompts, C=8192.
+    """
+    rng = np.random.default_rng(1000 + index)
+    if index == 0:
+        return make_chain_case(1, 20480, 2048, 37, seed=seed, dtype=dtype, guard=guard, miss_frac=(0.1, 0.1))
+    if index == 1:
+        tails = rng.integers(1, 128, size=24)
+        return make_chain_case(24, 32768, 2048, tails, seed=seed, dtype=dtype, guard=guard)
+    if index == 2:
+        lens = (rng.integers(20480, 65536 + 1, size=64) // BLOCK) * BLOCK
+        tails = rng.integers(1, 128, size=64)
+        return make_chain_case(64, lens, 2048, tails, seed=seed, dtype=dtype, guard=guard)
+    if index == 3:
+        tails = rng.integers(4, 128, size=16)
+        return make_chain_case(16, 49152, 8192, tails, seed=seed, dtype=dtype, guard=guard, mtp=True)
+    raise ValueError(f"no baseline config {index}")

@@ -1,0 +1,216 @@
+"""fused_li_manage / fused_li_manage_mtp on the GPU vs the oracle.
+
+* closed-form index (score == token id, ut_ops/test_fused_li_manage.py:146-173)
+  with the reference's structured cache state, 32 and 64 index heads, a
+  source that crosses the 18-bit boundary (262272 tokens, the reference
+  default ``--seq-lens``), the behavioural invariants and the repeated update;
+* random margin-guarded workloads: every integer output and the updated pool
+  bit-exact against the oracle, bf16 and fp16;
+* MTP3 union bookkeeping bit-exact;
+* row guards: invalid rows only get miss_counts = 0.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import ints, oracle_lim
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOPK = 2048
+
+
+def _run_lim(dcase, mtp=False):
+    from nanovllm_amd import dsa_offload_ops as ops
+
+    t = dcase.tensors
+    if mtp:
+        ops.fused_li_manage_mtp(t["query_index"], t["index_weights"], t["index_key_cache"], t["index_block_table"],
+                                t["num_candidate_tokens"], t["num_cache_tokens"], t["req_pool_entries"],
+                                t["cache_slots_pool"], t["topk_src_ids"], t["topk_dst_slots"], t["miss_src_ids"],
+                                t["miss_dst_slots"], t["miss_counts"])
+    else:
+        ops.fused_li_manage(t["query_index"], t["index_weights"], t["index_key_cache"], t["index_block_table"],
+                            t["num_candidate_tokens"], t["num_cache_tokens"], t["req_pool_entries"],
+                            t["cache_slots_pool"], t["topk_src_ids"], t["topk_dst_slots"], t["miss_counts"])
+    torch.cuda.synchronize()
+
+
+def _structured_case(heads, batch, seq_len, cache_tokens, miss_count, seed=7):
+    """The reference's build_case (test_fused_li_manage.py:127-243)."""
+    from nanovllm_amd.workloads import ChainCase
+
+    blocks = (seq_len + 127) // 128
+    cap = blocks * 128
+    q = torch.zeros(batch, heads, 128)
+    q[:, 0, :4] = torch.tensor([1.0, 64.0, 4096.0, 262144.0])
+    w = torch.zeros(batch, heads)
+    w[:, 0] = 1
+    ids = torch.arange(cap)
+    key = torch.zeros(batch, blocks, 128, 1, 128)
+    key[..., 0, 0] = (ids % 64).view(blocks, 128).float()
+    key[..., 0, 1] = ((ids // 64) % 64).view(blocks, 128).float()
+    key[..., 0, 2] = ((ids // 4096) % 64).view(blocks, 128).float()
+    key[..., 0, 3] = (ids // 262144).view(blocks, 128).float()
+    table = torch.arange(batch * blocks, dtype=torch.int32).view(batch, blocks)
+    pool_size = batch + 1
+    entries = torch.arange(batch, 0, -1, dtype=torch.int32)
+    pool = torch.full((pool_size, cap), -1, dtype=torch.int32)
+    topk = np.arange(seq_len - TOPK, seq_len)
+    hit = topk[miss_count:]
+    other_count = cache_tokens - hit.size
+    lower = seq_len - TOPK
+    others = (np.arange(other_count) * lower) // other_count if other_count else np.zeros(0, np.int64)
+    cached = torch.from_numpy(np.concatenate([hit, others]))
+    g = torch.Generator().manual_seed(seed)
+    for row in range(batch):
+        pool[int(entries[row]), cached] = torch.randperm(cache_tokens, generator=g, dtype=torch.int32)
+    t = {
+        "query_index": q.to(torch.bfloat16), "index_weights": w.to(torch.bfloat16),
+        "index_key_cache": key.view(batch * blocks, 128, 1, 128).to(torch.bfloat16), "index_block_table": table,
+        "num_candidate_tokens": torch.full((batch,), seq_len, dtype=torch.int32),
+        "num_cache_tokens": torch.full((batch,), cache_tokens, dtype=torch.int32), "req_pool_entries": entries,
+        "cache_slots_pool": pool, "topk_src_ids": torch.full((batch, 1, TOPK), -1, dtype=torch.int32),
+        "topk_dst_slots": torch.full((batch, 1, TOPK), -1, dtype=torch.int32),
+        "miss_counts": torch.full((batch,), -1, dtype=torch.int32),
+    }
+    return ChainCase(t, {})
+
+
+def _validate(dcase, old_pool, seq_len, cache_tokens, expected_miss):
+    """Port of validate_outputs (test_fused_li_manage.py:314-426)."""
+    t = dcase.tensors
+    B = t["num_candidate_tokens"].numel()
+    counts = ints(t["miss_counts"])
+    assert counts.tolist() == [expected_miss] * B
+    src = ints(t["topk_src_ids"]).reshape(B, TOPK).astype(np.int64)
+    dst = ints(t["topk_dst_slots"]).reshape(B, TOPK).astype(np.int64)
+    pool = ints(t["cache_slots_pool"])
+    entries = ints(t["req_pool_entries"])
+    for r in range(pool.shape[0]):
+        if r not in set(entries.tolist()):
+            assert np.array_equal(pool[r], old_pool[r]), f"unmapped pool row {r} modified"
+    for b in range(B):
+        s, d = src[b], dst[b]
+        assert np.array_equal(np.sort(s), np.arange(seq_len - TOPK, seq_len))
+        assert d.min() >= 0 and d.max() < cache_tokens and np.unique(d).size == TOPK
+        old = old_pool[entries[b]][s]
+        miss = old == -1
+        assert miss[:expected_miss].all() and not miss[expected_miss:].any()
+        assert np.array_equal(d[expected_miss:], old[expected_miss:])
+        assert np.array_equal(pool[entries[b]][s], d)
+        valid = pool[entries[b]][pool[entries[b]] >= 0]
+        assert valid.size == cache_tokens and np.unique(valid).size == cache_tokens
+    return pool
+
+
+@pytest.mark.parametrize("heads,batch,seq_len,cache_tokens,miss", [
+    (32, 2, 20480, 2048, 205),
+    (64, 2, 20480, 2048, 205),
+    (32, 1, 262272, 6144, 300),
+    (64, 3, 65536, 8192, 150),
+])
+def test_lim_closed_form_and_repeat(heads, batch, seq_len, cache_tokens, miss):
+    print(f"LIM closed-form heads={heads} B={batch} N={seq_len} C={cache_tokens} miss={miss}", flush=True)
+    case = _structured_case(heads, batch, seq_len, cache_tokens, miss)
+    expect = oracle_lim(case)
+    old_pool = ints(case["cache_slots_pool"])
+    d = case.to_device("cuda")
+    _run_lim(d)
+    pool1 = _validate(d, old_pool, seq_len, cache_tokens, miss)
+    assert np.array_equal(ints(d["topk_src_ids"]), expect["src"])
+    assert np.array_equal(ints(d["topk_dst_slots"]), expect["dst"])
+    assert np.array_equal(pool1, expect["pool"])
+    if seq_len > (1 << 18):
+        assert ints(d["topk_src_ids"]).max() >= (1 << 18)
+    _run_lim(d)  # same query again: everything is cached now
+    _validate(d, pool1, seq_len, cache_tokens, 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("heads", [32, 64])
+def test_lim_random_bit_exact(dtype, heads):
+    from nanovllm_amd.workloads import make_chain_case
+
+    case = make_chain_case(4, [4096, 6144, 8192, 5120], [2048, 3072, 2560, 2048], [5, 9, 100, 1], index_heads=heads,
+                           seed=11 + heads, dtype=dtype)
+    print(f"LIM random {dtype} heads={heads} halvings={case.meta['halvings']} miss={case.meta['miss_target']}",
+          flush=True)
+    expect = oracle_lim(case)
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d)
+    assert np.array_equal(ints(d["miss_counts"]), expect["miss_counts"])
+    assert np.array_equal(ints(d["topk_src_ids"]), expect["src"])
+    assert np.array_equal(ints(d["topk_dst_slots"]), expect["dst"])
+    assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
+    assert expect["miss_counts"].sum() > 0
+
+
+@pytest.mark.parametrize("heads", [32, 64])
+def test_lim_mtp_bit_exact(heads):
+    from nanovllm_amd.workloads import make_chain_case
+
+    case = make_chain_case(3, [9216, 12288, 16384], [8192, 9216, 8320], [4, 10, 60], index_heads=heads, seed=5,
+                           mtp=True)
+    print(f"LIM MTP heads={heads} halvings={case.meta['halvings']} miss={case.meta['miss_target']}", flush=True)
+    expect = oracle_lim(case, mtp=True)
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d, mtp=True)
+    mc = ints(d["miss_counts"])
+    assert np.array_equal(mc, expect["miss_counts"])
+    assert np.array_equal(ints(d["topk_src_ids"]), expect["src"])
+    assert np.array_equal(ints(d["topk_dst_slots"]), expect["dst"])
+    ms, md = ints(d["miss_src_ids"]), ints(d["miss_dst_slots"])
+    for b in range(mc.size):
+        assert np.array_equal(ms[b, :mc[b]], expect["miss_src"][b, :mc[b]])
+        assert np.array_equal(md[b, :mc[b]], expect["miss_dst"][b, :mc[b]])
+    assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
+
+
+def test_lim_row_guards():
+    from nanovllm_amd.workloads import make_chain_case
+
+    case = make_chain_case(5, 4096, 2048, 8, seed=3)
+    t = case.tensors
+    t["num_candidate_tokens"][0] = 0          # no candidates
+    t["num_cache_tokens"][1] = 0              # C == 0
+    t["num_cache_tokens"][2] = 1024           # C < 2048
+    t["num_cache_tokens"][3] = 8192           # C > candidates
+    t["req_pool_entries"][4] = 99             # pool row out of range
+    before = ints(t["cache_slots_pool"])
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d)
+    assert ints(d["miss_counts"]).tolist() == [0] * 5
+    assert np.array_equal(ints(d["cache_slots_pool"]), before)
+    assert np.all(ints(d["topk_src_ids"]) == -1)
+
+
+def test_lim_meta_and_errors():
+    from nanovllm_amd import dsa_offload_ops as ops
+
+    meta = torch.device("meta")
+    B = 2
+    args = [torch.empty(B, 32, 128, dtype=torch.bfloat16, device=meta), torch.empty(B, 32, dtype=torch.bfloat16,
+            device=meta), torch.empty(8, 128, 1, 128, dtype=torch.bfloat16, device=meta),
+            torch.empty(B, 4, dtype=torch.int32, device=meta)] + [torch.empty(B, dtype=torch.int32, device=meta)] * 3 + [
+            torch.empty(3, 512, dtype=torch.int32, device=meta), torch.empty(B, 1, TOPK, dtype=torch.int32, device=meta),
+            torch.empty(B, 1, TOPK, dtype=torch.int32, device=meta), torch.empty(B, dtype=torch.int32, device=meta)]
+    assert ops.fused_li_manage(*args) is None
+    case = make_bad = None  # noqa: F841
+    from nanovllm_amd.workloads import make_chain_case
+
+    d = make_chain_case(1, 4096, 2048, 8, seed=1).to_device("cuda", host_mapped=False)
+    t = d.tensors
+    with pytest.raises(RuntimeError, match="32 or 64"):
+        ops.fused_li_manage(t["query_index"][:, :16].contiguous(), t["index_weights"][:, :16].contiguous(),
+                            t["index_key_cache"], t["index_block_table"], t["num_candidate_tokens"],
+                            t["num_cache_tokens"], t["req_pool_entries"], t["cache_slots_pool"], t["topk_src_ids"],
+                            t["topk_dst_slots"], t["miss_counts"])
+    with pytest.raises(RuntimeError, match="state width"):
+        ops.fused_li_manage(t["query_index"], t["index_weights"], t["index_key_cache"], t["index_block_table"],
+                            t["num_candidate_tokens"], t["num_cache_tokens"], t["req_pool_entries"],
+                            t["cache_slots_pool"][:, :128].contiguous(), t["topk_src_ids"], t["topk_dst_slots"],
+                            t["miss_counts"])
