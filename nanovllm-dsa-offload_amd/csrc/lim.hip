@@ -8,7 +8,7 @@
 //      (staged once per workgroup in LDS), fp32 accumulation, then ReLU,
 //      per-head weight and head reduction in registers.  Scores go to an fp32
 //      workspace row per query; the key scan is the only large HBM stream.
-//   2. lim_manage_kernel(_mtp) — one 1024-thread workgroup per request:
+//   2. lim_manage_kernel(_mtp) — one 512-thread workgroup per request:
 //      radix select of the top-2048 threshold on the scores, one ordered
 //      pass over the candidates against the request's pool row, victim
 //      selection, pairing and pool update.
@@ -31,6 +31,7 @@
 //      (ops/fused_li_manage_mtp/op_kernel/nanovllm_fused_li_manage_mtp.cpp,
 //       ut_ops/test_fused_li_manage_mtp.py:789-960).
 #include <cfloat>
+#include <climits>
 
 #include "nvdsa_common.h"
 #include "nvdsa_kernels.h"
@@ -40,7 +41,9 @@ namespace {
 
 constexpr int kScoreWaves = 4;                  // waves per score workgroup
 constexpr int kQStride = kIndexDim + 8;         // padded LDS row (bank spread)
-constexpr int kManageThreads = 1024;
+constexpr int kManageThreads = 512;
+constexpr int kBins = 2048;                       // radix histogram bins (11 bits)
+constexpr int kBinsPerThread = kBins / kManageThreads;
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr uint32_t kStateShift = 24;
 constexpr uint32_t kStateFree = 0;
@@ -170,56 +173,124 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
 }
 
 // ---------------------------------------------------------------------------
-// Block-wide helpers for the 1024-thread manage kernels.
+// Block-wide helpers for the 512-thread manage kernels.
+
+constexpr int kItems = 8;                          // consecutive tokens per thread in ordered passes
+constexpr int kChunk = kManageThreads * kItems;    // tokens per ordered chunk
+constexpr int kSlotItems = 4;                      // consecutive slots per thread in slot passes
+constexpr int kSlotChunk = kManageThreads * kSlotItems;
 
 struct SelectOut {
   uint32_t thresh;  // key of the k-th largest element
   int need_eq;      // elements equal to thresh that belong to the selection
-  int cnt_eq;       // elements equal to thresh
+  int cnt_eq;       // elements equal to thresh (INT_MAX when not counted)
 };
 
-// k-th largest 32-bit key among included elements of [0, n) by an
-// 11/11/10-bit radix select.  Requires (#included) >= k >= 1.
-template <typename KeyFn>
-__device__ SelectOut select_top(int n, int k, KeyFn key_of, uint32_t* hist, int* scratch, int* bcast) {
-  uint32_t prefix = 0, pmask = 0;
-  int remaining = k;
-  int cnt_eq = 0;
+__device__ inline uint32_t score_key(float s) { return float_key(s == 0.f ? 0.f : s); }
+
+// Block-wide min / max of 32-bit keys (every thread gets the result).
+__device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    lo = min(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), d, 64)));
+    hi = max(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), d, 64)));
+  }
+  const int wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * wid] = lo;
+    red[2 * wid + 1] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t l = red[0], h = red[1];
+    for (int w = 1; w < nw; ++w) {
+      l = min(l, red[2 * w]);
+      h = max(h, red[2 * w + 1]);
+    }
+    red[2 * nw] = l;
+    red[2 * nw + 1] = h;
+  }
+  __syncthreads();
+  lo = red[2 * nw];
+  hi = red[2 * nw + 1];
+  __syncthreads();
+}
+
+// k-th largest key among included keys, all of which lie in [kmin, kmax].
+// The radix passes work on key - kmin and start at the top bit of the range,
+// so the first 11-bit histogram already spreads over all 2048 bins (scores
+// share sign and exponent bits; a histogram of the raw top bits would pile
+// them into a few bins).  load(i, key[4], inc[4]) supplies group i < ngroups.
+// Requires (#included) >= k >= 1.
+template <typename Visit>
+__device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Visit visit, uint32_t* hist,
+                                        int* scratch, int* bcast) {
+  if (kmax == kmin) return SelectOut{kmin, k, INT_MAX};
   const int tid = threadIdx.x;
+  const int L = 32 - __clz(static_cast<int>(kmax - kmin));
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = k, cnt_eq = 0;
 #pragma unroll 1
-  for (int p = 0; p < 3; ++p) {
-    const int shift = p == 0 ? 21 : (p == 1 ? 10 : 0);
-    const uint32_t dmask = p == 2 ? 0x3ffu : 0x7ffu;
-    for (int i = tid; i < 2048; i += kManageThreads) hist[i] = 0;
+  for (int hi = L; hi > 0; hi -= 11) {
+    const int lo = hi > 11 ? hi - 11 : 0;
+    const uint32_t dmask = (1u << (hi - lo)) - 1u;
+    for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < n; i += kManageThreads) {
-      uint32_t key;
-      if (!key_of(i, key)) continue;
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & dmask], 1u);
+    visit([&](uint32_t key) {
+      const uint32_t d = key - kmin;
+      if ((d & pmask) == prefix) atomicAdd(&hist[(d >> lo) & dmask], 1u);
+    });
+    __syncthreads();
+    // Thread tid owns bins [tb*kBinsPerThread, +kBinsPerThread), threads in
+    // descending bin order; find the bin holding the remaining-th largest.
+    const int tb = kManageThreads - 1 - tid;
+    int cnt[kBinsPerThread];
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < kBinsPerThread; ++j) {
+      cnt[j] = static_cast<int>(hist[tb * kBinsPerThread + j]);
+      sum += cnt[j];
     }
-    __syncthreads();
-    const int tb = kManageThreads - 1 - tid;  // descending bin pairs
-    const int hi = static_cast<int>(hist[2 * tb + 1]);
-    const int lo = static_cast<int>(hist[2 * tb]);
     int total;
-    const int above = block_exclusive_scan(hi + lo, scratch, &total);
-    if (above < remaining && remaining <= above + hi) {
-      bcast[0] = 2 * tb + 1;
-      bcast[1] = above;
-      bcast[2] = hi;
-    } else if (above + hi < remaining && remaining <= above + hi + lo) {
-      bcast[0] = 2 * tb;
-      bcast[1] = above + hi;
-      bcast[2] = lo;
+    int acc = block_exclusive_scan(sum, scratch, &total);
+#pragma unroll
+    for (int j = kBinsPerThread - 1; j >= 0; --j) {
+      if (acc < remaining && remaining <= acc + cnt[j]) {
+        bcast[0] = tb * kBinsPerThread + j;
+        bcast[1] = acc;
+        bcast[2] = cnt[j];
+      }
+      acc += cnt[j];
     }
     __syncthreads();
-    prefix |= static_cast<uint32_t>(bcast[0]) << shift;
-    pmask |= dmask << shift;
+    prefix |= static_cast<uint32_t>(bcast[0]) << lo;
+    pmask |= dmask << lo;
     remaining -= bcast[1];
     cnt_eq = bcast[2];
     __syncthreads();
   }
-  return SelectOut{prefix, remaining, cnt_eq};
+  return SelectOut{prefix + kmin, remaining, cnt_eq};
+}
+
+// Same, with the keys supplied in groups of four: load(i, key[4], inc[4])
+// for group i < ngroups, groups strided over the workgroup.
+template <typename Load>
+__device__ SelectOut radix_select(int ngroups, int k, uint32_t kmin, uint32_t kmax, Load load, uint32_t* hist,
+                                  int* scratch, int* bcast) {
+  return radix_select_visit(
+      k, kmin, kmax,
+      [&](auto&& fn) {
+        for (int i = threadIdx.x; i < ngroups; i += kManageThreads) {
+          uint32_t key[4];
+          bool inc[4];
+          load(i, key, inc);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (inc[e]) fn(key[e]);
+        }
+      },
+      hist, scratch, bcast);
 }
 
 __device__ inline int block_sum(int v, int* scratch) {
@@ -229,7 +300,7 @@ __device__ inline int block_sum(int v, int* scratch) {
 }
 
 // Exclusive block scan of four packed 16-bit counters (each chunk total must
-// stay below 65536, which holds for 1024 threads).
+// stay below 65536: at most kChunk per chunk here).
 __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, uint64_t* total) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -261,50 +332,127 @@ __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, 
 
 __device__ inline int lane16(uint64_t v, int q) { return static_cast<int>((v >> (16 * q)) & 0xffffu); }
 
-__device__ inline uint32_t score_key(float s) { return float_key(s == 0.f ? 0.f : s); }
+// Score keys of tokens [t, t + 4) of one score row (tokens >= n excluded).
+__device__ inline void load_score_keys(const float* s, int n, int t, uint32_t* key, bool* inc) {
+  if (t + 3 < n) {
+    const float4 v = *reinterpret_cast<const float4*>(s + t);
+    key[0] = score_key(v.x);
+    key[1] = score_key(v.y);
+    key[2] = score_key(v.z);
+    key[3] = score_key(v.w);
+    inc[0] = inc[1] = inc[2] = inc[3] = true;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      inc[e] = t + e < n;
+      key[e] = inc[e] ? score_key(s[t + e]) : 0u;
+    }
+  }
+}
+
+// Eight consecutive tokens [t0, t0 + 8): score keys and pool slots.
+__device__ inline void load_tokens8(const float* s, const int32_t* pool, int n, int t0, uint32_t* u, int32_t* slot,
+                                    bool* in) {
+  if (t0 + kItems <= n) {
+    const float4 a = *reinterpret_cast<const float4*>(s + t0);
+    const float4 b = *reinterpret_cast<const float4*>(s + t0 + 4);
+    const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
+    const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
+    u[0] = score_key(a.x); u[1] = score_key(a.y); u[2] = score_key(a.z); u[3] = score_key(a.w);
+    u[4] = score_key(b.x); u[5] = score_key(b.y); u[6] = score_key(b.z); u[7] = score_key(b.w);
+    slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
+    slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) in[e] = true;
+  } else {
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      in[e] = t0 + e < n;
+      u[e] = in[e] ? score_key(s[t0 + e]) : 0u;
+      slot[e] = in[e] ? pool[t0 + e] : -1;
+    }
+  }
+}
 
 // Victim slots: the m non-hit slots of [0, c) with the smallest key (free
 // slots first), ascending slot on ties, written in ascending slot order to
 // vslot[0..min(m, #non-hit)).  Returns the number written.
-__device__ int select_victims(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot, uint32_t* hist,
-                              int* scratch, int* bcast) {
+__device__ __forceinline__ int select_victims(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot, uint32_t* hist,
+                              int* scratch, int* bcast, uint32_t* red) {
   const int tid = threadIdx.x;
   if (m <= 0) return 0;
-  int local = 0;
-  for (int i = tid; i < c; i += kManageThreads) local += (stab[i] >> kStateShift) != kStateHit;
-  const int nonhit = block_sum(local, scratch);
-  const bool take_all = m >= nonhit;
+  // inverted keys: the smallest score is the largest inverted key; free slots
+  // (key 0 before inversion) rank first.
   auto inv_key = [&](int i, uint32_t& key) -> bool {
     const uint32_t st = stab[i] >> kStateShift;
     if (st == kStateHit) return false;
     key = ~(st == kStateFree ? 0u : skey[i]);
     return true;
   };
+  int local = 0;
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int i = tid; i < c; i += kManageThreads) {
+    uint32_t key;
+    if (inv_key(i, key)) {
+      ++local;
+      lo = min(lo, key);
+      hi = max(hi, key);
+    }
+  }
+  const int nonhit = block_sum(local, scratch);
+  block_minmax(lo, hi, red);
+  const bool take_all = m >= nonhit;
   SelectOut sel{0, 0, 0};
-  if (!take_all) sel = select_top(c, m, inv_key, hist, scratch, bcast);
+  if (!take_all) {
+    sel = radix_select(
+        static_cast<int>(ceil_div(c, 4)), m, lo, hi,
+        [&](int g, uint32_t* key, bool* inc) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g + e;
+            inc[e] = i < c && inv_key(i, key[e]);
+          }
+        },
+        hist, scratch, bcast);
+  }
   const bool need_rank = !take_all && sel.cnt_eq != sel.need_eq;
   int run = 0, eq_run = 0;
-  for (int base = 0; base < c; base += kManageThreads) {
-    const int i = base + tid;
-    uint32_t key = 0;
-    const bool nonhit_i = i < c && inv_key(i, key);
-    bool victim;
-    if (take_all) {
-      victim = nonhit_i;
-    } else {
-      const bool gt = nonhit_i && key > sel.thresh;
-      const bool eq = nonhit_i && key == sel.thresh;
-      victim = gt || (eq && !need_rank);
-      if (need_rank) {
-        int tot;
-        const int rk = block_exclusive_scan(eq ? 1 : 0, scratch, &tot);
-        victim = gt || (eq && eq_run + rk < sel.need_eq);
-        eq_run += tot;
+  for (int base = 0; base < c; base += kSlotChunk) {
+    const int i0 = base + tid * kSlotItems;
+    unsigned vmask = 0, eqmask = 0;
+#pragma unroll
+    for (int e = 0; e < kSlotItems; ++e) {
+      uint32_t key = 0;
+      const bool nh = i0 + e < c && inv_key(i0 + e, key);
+      if (take_all) {
+        if (nh) vmask |= 1u << e;
+      } else if (nh) {
+        if (key > sel.thresh) vmask |= 1u << e;
+        if (key == sel.thresh) {
+          if (need_rank) eqmask |= 1u << e;
+          else vmask |= 1u << e;
+        }
       }
     }
+    if (need_rank) {
+      int tot;
+      int r = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
+#pragma unroll
+      for (int e = 0; e < kSlotItems; ++e)
+        if ((eqmask >> e) & 1u) {
+          if (r < sel.need_eq) vmask |= 1u << e;
+          ++r;
+        }
+      eq_run += tot;
+    }
     int tot;
-    const int vp = block_exclusive_scan(victim ? 1 : 0, scratch, &tot);
-    if (victim && run + vp < m) vslot[run + vp] = i;
+    int pos = run + block_exclusive_scan(__popc(vmask), scratch, &tot);
+#pragma unroll
+    for (int e = 0; e < kSlotItems; ++e)
+      if ((vmask >> e) & 1u) {
+        if (pos < m) vslot[pos] = i0 + e;
+        ++pos;
+      }
     run += tot;
   }
   __syncthreads();
@@ -313,9 +461,127 @@ __device__ int select_victims(int c, int m, const uint32_t* stab, const uint32_t
 
 // ---------------------------------------------------------------------------
 // 2a. MTP0 management.
+
+// Classify eight consecutive candidates [t0, t0 + 8) of the ordered pass:
+// selection (with ascending-token tie ranks), misses appended in token order,
+// cached tokens recorded in the slot table.  Contains block scans.
+__device__ inline void mtp0_classify8(int t0, const uint32_t* u, const int32_t* slot, const bool* in, int c,
+                                      const SelectOut& sel, bool need_rank, int& eq_run, int& miss_run,
+                                      int32_t* misses, uint32_t* stab, uint32_t* skey, int* scratch) {
+  unsigned selmask = 0, eqmask = 0, cachedmask = 0;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    if (!in[e]) continue;
+    if (u[e] > sel.thresh) selmask |= 1u << e;
+    if (u[e] == sel.thresh) {
+      if (need_rank) eqmask |= 1u << e;
+      else selmask |= 1u << e;
+    }
+    if (slot[e] >= 0 && slot[e] < c) cachedmask |= 1u << e;
+  }
+  if (need_rank) {
+    int tot;
+    int rk = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e)
+      if ((eqmask >> e) & 1u) {
+        if (rk < sel.need_eq) selmask |= 1u << e;
+        ++rk;
+      }
+    eq_run += tot;
+  }
+  const unsigned missmask = selmask & ~cachedmask;
+  int tot;
+  int mp = miss_run + block_exclusive_scan(__popc(missmask), scratch, &tot);
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    if ((missmask >> e) & 1u) misses[mp++] = t0 + e;
+    if ((cachedmask >> e) & 1u) {
+      if ((selmask >> e) & 1u) {
+        stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
+      } else {
+        stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
+        skey[slot[e]] = u[e];
+      }
+    }
+  }
+  miss_run += tot;
+}
+
+__device__ inline void load_pool8(const int32_t* pool, int n, int t0, int32_t* slot) {
+  if (t0 + kItems <= n) {
+    const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
+    const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
+    slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
+    slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) slot[e] = t0 + e < n ? pool[t0 + e] : -1;
+  }
+}
+
+// Victims, pairing, pool update and the output row of one MTP0 request.
+__device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int m, int32_t* pool, uint32_t* stab, uint32_t* skey,
+                            const int32_t* misses, int* vslot, uint32_t* hist, int* scratch, int* bcast,
+                            uint32_t* red) {
+  const int tid = threadIdx.x;
+  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
+  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
+  const int nv = select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
+  // Misses first (ascending token), paired with ascending victim slots.
+  for (int i = tid; i < m; i += kManageThreads) {
+    const int t = misses[i];
+    const int d = i < nv ? vslot[i] : -1;
+    out_src[i] = t;
+    out_dst[i] = d;
+    if (d >= 0) {
+      const uint32_t e = stab[d];
+      if ((e >> kStateShift) == kStateCand) pool[e & kTokenMask] = -1;
+      pool[t] = d;
+    }
+  }
+  // Hits by descending old slot: position p of the descending scan is slot c-1-p.
+  int hit_run = 0;
+  for (int base = 0; base < c; base += kSlotChunk) {
+    const int p0 = base + tid * kSlotItems;
+    unsigned hmask = 0;
+    uint32_t ent[kSlotItems];
+#pragma unroll
+    for (int e = 0; e < kSlotItems; ++e) {
+      const int i = c - 1 - (p0 + e);
+      ent[e] = i >= 0 ? stab[i] : 0u;
+      if (i >= 0 && (ent[e] >> kStateShift) == kStateHit) hmask |= 1u << e;
+    }
+    int tot;
+    int pos = m + hit_run + block_exclusive_scan(__popc(hmask), scratch, &tot);
+#pragma unroll
+    for (int e = 0; e < kSlotItems; ++e)
+      if ((hmask >> e) & 1u) {
+        if (pos < kTopK) {
+          out_src[pos] = static_cast<int32_t>(ent[e] & kTokenMask);
+          out_dst[pos] = c - 1 - (p0 + e);
+        }
+        ++pos;
+      }
+    hit_run += tot;
+  }
+  // Positions a corrupt pool (duplicate slots) left unfilled.
+  for (int pos = m + hit_run + tid; pos < kTopK; pos += kManageThreads) {
+    out_src[pos] = -1;
+    out_dst[pos] = -1;
+  }
+  if (tid == 0) a.miss_counts[b] = m;
+}
+
+// RES > 0: the request's scores live in registers, RES chunks of kChunk
+// tokens (thread t holds tokens ch*kChunk + 8t .. +8), read from memory once;
+// the radix passes then touch no memory.  RES == 0 streams the scores from
+// the workspace on every pass (any source length).
+template <int RES>
 __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, LimWs w) {
-  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kTopK];
   const int b = blockIdx.x;
@@ -333,90 +599,100 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kSlotStride;
   uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kSlotStride;
   int32_t* misses = w.miss_list + static_cast<int64_t>(b) * kUnionCap;
-  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
-  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
-  const SelectOut sel = select_top(
-      n, kTopK, [&](int i, uint32_t& key) { key = score_key(s[i]); return true; }, hist, scratch, bcast);
-  const bool need_rank = sel.cnt_eq != sel.need_eq;
-
-  // Ordered pass over the candidates.
   int eq_run = 0, miss_run = 0;
-  for (int base = 0; base < n; base += kManageThreads) {
-    const int t = base + tid;
-    const bool in = t < n;
-    const uint32_t u = in ? score_key(s[t]) : 0u;
-    const bool gt = in && u > sel.thresh;
-    const bool eq = in && u == sel.thresh;
-    bool chosen = gt || (eq && !need_rank);
-    if (need_rank) {
-      int tot;
-      const int rk = block_exclusive_scan(eq ? 1 : 0, scratch, &tot);
-      chosen = gt || (eq && eq_run + rk < sel.need_eq);
-      eq_run += tot;
-    }
-    const int32_t slot = in ? pool[t] : -1;
-    const bool cached = slot >= 0 && slot < c;
-    const bool miss = chosen && !cached;
-    int tot;
-    const int mp = block_exclusive_scan(miss ? 1 : 0, scratch, &tot);
-    if (miss) misses[miss_run + mp] = t;
-    miss_run += tot;
-    if (cached) {
-      if (chosen) {
-        stab[slot] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
+  if constexpr (RES > 0) {
+    uint32_t u[RES][kItems];
+    uint32_t lo = 0xffffffffu, hi = 0u;
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch) {
+      const int t0 = ch * kChunk + tid * kItems;
+      if (t0 + kItems <= n) {
+        const float4 x = *reinterpret_cast<const float4*>(s + t0);
+        const float4 y = *reinterpret_cast<const float4*>(s + t0 + 4);
+        u[ch][0] = score_key(x.x); u[ch][1] = score_key(x.y); u[ch][2] = score_key(x.z); u[ch][3] = score_key(x.w);
+        u[ch][4] = score_key(y.x); u[ch][5] = score_key(y.y); u[ch][6] = score_key(y.z); u[ch][7] = score_key(y.w);
       } else {
-        stab[slot] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
-        skey[slot] = u;
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) u[ch][e] = t0 + e < n ? score_key(s[t0 + e]) : 0u;
       }
+    }
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch)
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (ch * kChunk + tid * kItems + e < n) {
+          lo = min(lo, u[ch][e]);
+          hi = max(hi, u[ch][e]);
+        }
+    block_minmax(lo, hi, red);
+    const SelectOut sel = radix_select_visit(
+        kTopK, lo, hi,
+        [&](auto&& fn) {
+#pragma unroll
+          for (int ch = 0; ch < RES; ++ch)
+#pragma unroll
+            for (int e = 0; e < kItems; ++e)
+              if (ch * kChunk + tid * kItems + e < n) fn(u[ch][e]);
+        },
+        hist, scratch, bcast);
+    const bool need_rank = sel.cnt_eq != sel.need_eq;
+    int32_t nxt[kItems];
+    load_pool8(pool, n, tid * kItems, nxt);
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch) {
+      const int base = ch * kChunk;
+      if (base >= n) break;  // uniform
+      int32_t slot[kItems];
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) slot[e] = nxt[e];
+      if (ch + 1 < RES && base + kChunk < n) load_pool8(pool, n, base + kChunk + tid * kItems, nxt);
+      const int t0 = base + tid * kItems;
+      bool in[kItems];
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) in[e] = t0 + e < n;
+      mtp0_classify8(t0, u[ch], slot, in, c, sel, need_rank, eq_run, miss_run, misses, stab, skey, scratch);
+    }
+  } else {
+    const int ngroups = static_cast<int>(ceil_div(n, 4));
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int g = tid; g < ngroups; g += kManageThreads) {
+      uint32_t key[4];
+      bool inc[4];
+      load_score_keys(s, n, 4 * g, key, inc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (inc[e]) {
+          lo = min(lo, key[e]);
+          hi = max(hi, key[e]);
+        }
+    }
+    block_minmax(lo, hi, red);
+    const SelectOut sel = radix_select(
+        ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); },
+        hist, scratch, bcast);
+    const bool need_rank = sel.cnt_eq != sel.need_eq;
+    for (int base = 0; base < n; base += kChunk) {
+      const int t0 = base + tid * kItems;
+      uint32_t u[kItems];
+      int32_t slot[kItems];
+      bool in[kItems];
+      load_tokens8(s, pool, n, t0, u, slot, in);
+      mtp0_classify8(t0, u, slot, in, c, sel, need_rank, eq_run, miss_run, misses, stab, skey, scratch);
     }
   }
   __syncthreads();
-  const int m = miss_run;
-  const int nv = select_victims(c, m, stab, skey, vslot, hist, scratch, bcast);
-
-  // Misses first (ascending token), paired with ascending victim slots.
-  for (int i = tid; i < m; i += kManageThreads) {
-    const int t = misses[i];
-    const int d = i < nv ? vslot[i] : -1;
-    out_src[i] = t;
-    out_dst[i] = d;
-    if (d >= 0) {
-      const uint32_t e = stab[d];
-      if ((e >> kStateShift) == kStateCand) pool[e & kTokenMask] = -1;
-      pool[t] = d;
-    }
-  }
-  // Hits by descending old slot.
-  int hit_run = 0;
-  for (int base = 0; base < c; base += kManageThreads) {
-    const int i = c - 1 - (base + tid);
-    const uint32_t e = i >= 0 ? stab[i] : 0u;
-    const bool hit = i >= 0 && (e >> kStateShift) == kStateHit;
-    int tot;
-    const int hp = block_exclusive_scan(hit ? 1 : 0, scratch, &tot);
-    const int pos = m + hit_run + hp;
-    if (hit && pos < kTopK) {
-      out_src[pos] = static_cast<int32_t>(e & kTokenMask);
-      out_dst[pos] = i;
-    }
-    hit_run += tot;
-  }
-  // Positions a corrupt pool (duplicate slots) left unfilled.
-  for (int pos = m + hit_run + tid; pos < kTopK; pos += kManageThreads) {
-    out_src[pos] = -1;
-    out_dst[pos] = -1;
-  }
-  if (tid == 0) a.miss_counts[b] = m;
+  mtp0_finish(a, b, c, miss_run, pool, stab, skey, misses, vslot, hist, scratch, bcast, red);
 }
 
 // ---------------------------------------------------------------------------
 // 2b. MTP3 management: union of the four top-2048 sets.
 __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs a, LimWs w) {
-  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kUnionCap];
   __shared__ uint32_t thr[kMtpQueries];
@@ -439,12 +715,27 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
   int32_t* miss_src = a.miss_src + static_cast<int64_t>(b) * kUnionCap;
   int32_t* miss_dst = a.miss_dst + static_cast<int64_t>(b) * kUnionCap;
+  const int ngroups = static_cast<int>(ceil_div(n, 4));
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   for (int q = 0; q < kMtpQueries; ++q) {
     const float* sq = s + q * cap;
-    const SelectOut sel = select_top(
-        n, kTopK, [&](int i, uint32_t& key) { key = score_key(sq[i]); return true; }, hist, scratch, bcast);
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int g = tid; g < ngroups; g += kManageThreads) {
+      uint32_t key[4];
+      bool inc[4];
+      load_score_keys(sq, n, 4 * g, key, inc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (inc[e]) {
+          lo = min(lo, key[e]);
+          hi = max(hi, key[e]);
+        }
+    }
+    block_minmax(lo, hi, red);
+    const SelectOut sel = radix_select(
+        ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(sq, n, 4 * g, key, inc); },
+        hist, scratch, bcast);
     if (tid == 0) {
       thr[q] = sel.thresh;
       need[q] = sel.need_eq;
@@ -457,21 +748,43 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   // Pass A: query masks, slot states, union misses per first-selecting query.
   int eq_run[kMtpQueries] = {0, 0, 0, 0};
   int gmiss[kMtpQueries] = {0, 0, 0, 0};
-  for (int base = 0; base < n; base += kManageThreads) {
-    const int t = base + tid;
-    const bool in = t < n;
-    uint32_t u[kMtpQueries];
-    uint32_t umax = 0;
-    uint64_t eqp = 0;
-    unsigned mask = 0;
+  for (int base = 0; base < n; base += kChunk) {
+    const int t0 = base + tid * kItems;
+    uint32_t u[kMtpQueries][kItems];
+    int32_t slot[kItems];
+    bool in[kItems];
+    load_tokens8(s, pool, n, t0, u[0], slot, in);
 #pragma unroll
-    for (int q = 0; q < kMtpQueries; ++q) {
-      u[q] = in ? score_key(s[q * cap + t]) : 0u;
-      umax = u[q] > umax ? u[q] : umax;
-      if (in && u[q] > thr[q]) mask |= 1u << q;
-      if (in && u[q] == thr[q]) {
-        if (rank_needed[q]) eqp |= uint64_t{1} << (16 * q);
-        else mask |= 1u << q;
+    for (int q = 1; q < kMtpQueries; ++q) {
+      const float* sq = s + q * cap;
+      if (t0 + kItems <= n) {
+        const float4 x = *reinterpret_cast<const float4*>(sq + t0);
+        const float4 y = *reinterpret_cast<const float4*>(sq + t0 + 4);
+        u[q][0] = score_key(x.x); u[q][1] = score_key(x.y); u[q][2] = score_key(x.z); u[q][3] = score_key(x.w);
+        u[q][4] = score_key(y.x); u[q][5] = score_key(y.y); u[q][6] = score_key(y.z); u[q][7] = score_key(y.w);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) u[q][e] = in[e] ? score_key(sq[t0 + e]) : 0u;
+      }
+    }
+    unsigned qmask[kItems];
+    uint64_t eqp = 0;
+    unsigned eqbits[kMtpQueries] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      qmask[e] = 0;
+      if (!in[e]) continue;
+#pragma unroll
+      for (int q = 0; q < kMtpQueries; ++q) {
+        if (u[q][e] > thr[q]) qmask[e] |= 1u << q;
+        if (u[q][e] == thr[q]) {
+          if (rank_needed[q]) {
+            eqbits[q] |= 1u << e;
+            eqp += uint64_t{1} << (16 * q);
+          } else {
+            qmask[e] |= 1u << q;
+          }
+        }
       }
     }
     if (any_rank) {
@@ -479,24 +792,44 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
       const uint64_t rk = block_exclusive_scan4(eqp, scratch64, &tot);
 #pragma unroll
       for (int q = 0; q < kMtpQueries; ++q) {
-        if ((eqp >> (16 * q)) & 1u)
-          if (eq_run[q] + lane16(rk, q) < need[q]) mask |= 1u << q;
+        int rq = eq_run[q] + lane16(rk, q);
+#pragma unroll
+        for (int e = 0; e < kItems; ++e)
+          if ((eqbits[q] >> e) & 1u) {
+            if (rq < need[q]) qmask[e] |= 1u << q;
+            ++rq;
+          }
         eq_run[q] += lane16(tot, q);
       }
     }
-    const int32_t slot = in ? pool[t] : -1;
-    const bool cached = slot >= 0 && slot < c;
-    if (in) masks[t] = static_cast<uint8_t>(mask);
-    if (cached) {
-      if (mask) {
-        stab[slot] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
-      } else {
-        stab[slot] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
-        skey[slot] = umax;
+    uint64_t missp = 0;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      if (!in[e]) continue;
+      const bool cached = slot[e] >= 0 && slot[e] < c;
+      if (cached) {
+        if (qmask[e]) {
+          stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
+        } else {
+          uint32_t umax = u[0][e];
+#pragma unroll
+          for (int q = 1; q < kMtpQueries; ++q) umax = u[q][e] > umax ? u[q][e] : umax;
+          stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
+          skey[slot[e]] = umax;
+        }
+      } else if (qmask[e]) {
+        missp += uint64_t{1} << (16 * __builtin_ctz(qmask[e]));
       }
     }
-    const int g = mask ? __builtin_ctz(mask) : 0;
-    const uint64_t missp = (mask && !cached) ? (uint64_t{1} << (16 * g)) : 0;
+    if (t0 + kItems <= n) {
+      const uint32_t m0 = qmask[0] | (qmask[1] << 8) | (qmask[2] << 16) | (qmask[3] << 24);
+      const uint32_t m1 = qmask[4] | (qmask[5] << 8) | (qmask[6] << 16) | (qmask[7] << 24);
+      *reinterpret_cast<uint2*>(masks + t0) = make_uint2(m0, m1);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (in[e]) masks[t0 + e] = static_cast<uint8_t>(qmask[e]);
+    }
     uint64_t tot;
     (void)block_exclusive_scan4(missp, scratch64, &tot);
 #pragma unroll
@@ -504,53 +837,96 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   }
   __syncthreads();
   const int m = gmiss[0] + gmiss[1] + gmiss[2] + gmiss[3];
-  const int gbase[kMtpQueries] = {0, gmiss[0], gmiss[0] + gmiss[1], gmiss[0] + gmiss[1] + gmiss[2]};
-  const int nv = select_victims(c, m, stab, skey, vslot, hist, scratch, bcast);
+  int gbase[kMtpQueries];
+  gbase[0] = 0;
+#pragma unroll
+  for (int q = 1; q < kMtpQueries; ++q) gbase[q] = gbase[q - 1] + gmiss[q - 1];
+  const int nv = select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
 
   // Pass B: union-ordered misses, per-query rows, pool update.
   int gm_run[kMtpQueries] = {0, 0, 0, 0};
   int row_run[kMtpQueries] = {0, 0, 0, 0};
-  for (int base = 0; base < n; base += kManageThreads) {
-    const int t = base + tid;
-    const bool in = t < n;
-    const unsigned mask = in ? masks[t] : 0u;
-    const int32_t slot = mask ? pool[t] : -1;
-    const bool cached = slot >= 0 && slot < c;
-    const bool miss = mask && !cached;
-    const int g = mask ? __builtin_ctz(mask) : 0;
-    uint64_t tot;
-    const uint64_t mrk = block_exclusive_scan4(miss ? (uint64_t{1} << (16 * g)) : 0, scratch64, &tot);
-    int new_slot = slot;
-    if (miss) {
-      const int pos = gbase[g] + gm_run[g] + lane16(mrk, g);
-      const int d = pos < nv ? vslot[pos] : -1;
-      miss_src[pos] = t;
-      miss_dst[pos] = d;
-      new_slot = d;
-      if (d >= 0) {
-        const uint32_t e = stab[d];
-        if ((e >> kStateShift) == kStateCand) pool[e & kTokenMask] = -1;
-        pool[t] = d;
+  for (int base = 0; base < n; base += kChunk) {
+    const int t0 = base + tid * kItems;
+    unsigned mb[kItems];
+    int32_t slot[kItems];
+    if (t0 + kItems <= n) {
+      const uint2 mm = *reinterpret_cast<const uint2*>(masks + t0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mb[e] = (mm.x >> (8 * e)) & 0xffu;
+        mb[e + 4] = (mm.y >> (8 * e)) & 0xffu;
+      }
+      const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
+      const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
+      slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
+      slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) {
+        const bool inb = t0 + e < n;
+        mb[e] = inb ? masks[t0 + e] : 0;
+        slot[e] = inb ? pool[t0 + e] : -1;
       }
     }
+    uint64_t missp = 0, rowp = 0;
 #pragma unroll
-    for (int q = 0; q < kMtpQueries; ++q) gm_run[q] += lane16(tot, q);
-    uint64_t rowp = 0;
+    for (int e = 0; e < kItems; ++e) {
+      const unsigned mk = mb[e];
+      if (!mk) continue;
+      const bool cached = slot[e] >= 0 && slot[e] < c;
+      if (!cached) missp += uint64_t{1} << (16 * __builtin_ctz(mk));
 #pragma unroll
-    for (int q = 0; q < kMtpQueries; ++q)
-      if ((mask >> q) & 1u) rowp |= uint64_t{1} << (16 * q);
-    const uint64_t rrk = block_exclusive_scan4(rowp, scratch64, &tot);
+      for (int q = 0; q < kMtpQueries; ++q)
+        if ((mk >> q) & 1u) rowp += uint64_t{1} << (16 * q);
+    }
+    uint64_t mtot, rtot;
+    const uint64_t mrk = block_exclusive_scan4(missp, scratch64, &mtot);
+    const uint64_t rrk = block_exclusive_scan4(rowp, scratch64, &rtot);
+    int mpos[kMtpQueries], rpos[kMtpQueries];
 #pragma unroll
     for (int q = 0; q < kMtpQueries; ++q) {
-      if ((mask >> q) & 1u) {
-        const int i = row_run[q] + lane16(rrk, q);
-        const int64_t row = static_cast<int64_t>(b) * kMtpQueries + q;
-        if (i < kTopK) {
-          a.topk_src[row * kTopK + i] = miss ? t : -1;
-          a.topk_dst[row * kTopK + i] = new_slot;
+      mpos[q] = gbase[q] + gm_run[q] + lane16(mrk, q);
+      rpos[q] = row_run[q] + lane16(rrk, q);
+    }
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      const unsigned mk = mb[e];
+      if (!mk) continue;
+      const int t = t0 + e;
+      const bool cached = slot[e] >= 0 && slot[e] < c;
+      int new_slot = slot[e];
+      if (!cached) {
+        const int g = __builtin_ctz(mk);
+        int pos = 0;
+#pragma unroll
+        for (int q = 0; q < kMtpQueries; ++q)
+          if (q == g) pos = mpos[q]++;
+        const int d = pos < nv ? vslot[pos] : -1;
+        miss_src[pos] = t;
+        miss_dst[pos] = d;
+        new_slot = d;
+        if (d >= 0) {
+          const uint32_t ent = stab[d];
+          if ((ent >> kStateShift) == kStateCand) pool[ent & kTokenMask] = -1;
+          pool[t] = d;
         }
       }
-      row_run[q] += lane16(tot, q);
+#pragma unroll
+      for (int q = 0; q < kMtpQueries; ++q)
+        if ((mk >> q) & 1u) {
+          const int i = rpos[q]++;
+          const int64_t row = static_cast<int64_t>(b) * kMtpQueries + q;
+          if (i < kTopK) {
+            a.topk_src[row * kTopK + i] = cached ? -1 : t;
+            a.topk_dst[row * kTopK + i] = new_slot;
+          }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kMtpQueries; ++q) {
+      gm_run[q] += lane16(mtot, q);
+      row_run[q] += lane16(rtot, q);
     }
   }
   if (tid == 0) a.miss_counts[b] = m;
@@ -572,8 +948,12 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   if (e != hipSuccess) return e;
   if (Q == 1) {
     prof_before(stream, kKernLimManage);
-    hipLaunchKernelGGL(lim_manage_kernel, dim3(static_cast<uint32_t>(a.batch)), dim3(kManageThreads), 0, stream, a,
-                       w);
+    const dim3 grid(static_cast<uint32_t>(a.batch)), block(kManageThreads);
+    if (a.source_capacity <= 8 * kChunk) {
+      hipLaunchKernelGGL(lim_manage_kernel<8>, grid, block, 0, stream, a, w);
+    } else {
+      hipLaunchKernelGGL(lim_manage_kernel<0>, grid, block, 0, stream, a, w);
+    }
   } else {
     prof_before(stream, kKernLimManageMtp);
     hipLaunchKernelGGL(lim_manage_mtp_kernel, dim3(static_cast<uint32_t>(a.batch)), dim3(kManageThreads), 0,

@@ -36,9 +36,12 @@ constexpr int kTileKeys = 32;
 constexpr int kAttnThreads = 256;
 constexpr int kHeadsPerBlock = 64;
 constexpr int kKStride = kQkDim + 8;       // LDS row of the key tile (elements)
-constexpr int kVStride = kTileKeys + 8;    // LDS row of the transposed value tile
+constexpr int kQStride = kQkDim + 8;       // LDS row of the staged queries
 constexpr int kChunksPerKey = kQkDim * 2 / 16;  // 72 x 16 bytes
-constexpr int kMaxSplits = 16;
+constexpr int kChunksPerThread = kTileKeys * kChunksPerKey / kAttnThreads;  // 9
+constexpr int kMaxSplits = 64;
+constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per window (one key per thread)
+constexpr int kWindowKeys = kWindowTiles * kTileKeys;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -89,9 +92,10 @@ Partials carve(void* ws, int64_t rows, int64_t splits, int64_t heads) {
 
 int choose_splits(int64_t rows, int64_t head_groups) {
   if (rows <= 0 || head_groups <= 0) return 1;
-  // Aim at ~2 resident workgroups per CU on 256 CUs.
-  const int64_t target = 512;
-  int64_t s = ceil_div(target, rows * head_groups);
+  // One resident workgroup per CU (the LDS footprint allows one): fill the
+  // 256 CUs in a single round.
+  const int64_t target = 256;
+  int64_t s = target / (rows * head_groups);
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
   return static_cast<int>(s);
@@ -99,12 +103,13 @@ int choose_splits(int64_t rows, int64_t head_groups) {
 
 template <typename T, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Partials part, int splits) {
-  __shared__ uint16_t ks[kTileKeys * kKStride];
-  __shared__ uint16_t vt[kCkvDim * kVStride];
-  __shared__ int64_t key_src[kTileKeys];   // source row (HBM or DRAM), -1 = masked
-  __shared__ int64_t key_dst[kTileKeys];   // HBM row a DRAM-sourced key is stored to, -1 = none
-  __shared__ int key_kind[kTileKeys];      // 0 masked, 1 HBM, 2 DRAM
-  __shared__ int key_use[kTileKeys];       // 1 when the key enters the softmax
+  __shared__ uint16_t qs[kHeadsPerBlock * kQStride];  // the block's 64 query rows (576 each)
+  __shared__ uint16_t ks[kTileKeys * kKStride];       // key tile, row-major
+  // Resolved keys of the current window of kWindowTiles tiles (one per thread):
+  // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to, flags.
+  __shared__ int64_t win_src[kWindowKeys];
+  __shared__ int64_t win_dst[kWindowKeys];
+  __shared__ int win_flag[kWindowKeys];  // bit 0: attend, bit 1: source is DRAM, bit 2: source valid
 
   const int64_t row = blockIdx.x / splits;
   const int split = static_cast<int>(blockIdx.x - row * splits);
@@ -129,21 +134,114 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   }
   const int list_len = plan.active ? plan.count : (FUSED ? copy_count : 0);
   const int ntiles = static_cast<int>(ceil_div(list_len, kTileKeys));
+  const int64_t pidx = (row * splits + split) * H + head;
 
-  // Query fragments for this wave: lane holds q[head][32*kk + 8*g .. +8].
-  uint4 qf[kQkDim / 32];
+  if (split >= ntiles) {  // nothing for this split (whole workgroup)
+    if (wave_active && head < a.heads && g == 0) {
+      part.ml[pidx * 2 + 0] = -INFINITY;
+      part.ml[pidx * 2 + 1] = 0.f;
+    }
+    return;
+  }
+
+  // Query rows of the block's heads -> LDS (zeros beyond H or for inactive rows).
   {
-    const uint4* qn = static_cast<const uint4*>(a.query) + (row * H + head) * (kCkvDim / 8);
-    const uint4* qr = static_cast<const uint4*>(a.query_rope) + (row * H + head) * (kKpeDim / 8);
-    const bool hv = wave_active && head < a.heads && plan.active;
-#pragma unroll
-    for (int kk = 0; kk < kQkDim / 32; ++kk) {
-      const int chunk = kk * 4 + g;  // 16-byte chunk index within the 576-dim row
+    const uint4* qn = static_cast<const uint4*>(a.query);
+    const uint4* qr = static_cast<const uint4*>(a.query_rope);
+    for (int i = tid; i < kHeadsPerBlock * kChunksPerKey; i += kAttnThreads) {
+      const int hh = i / kChunksPerKey;
+      const int c = i - hh * kChunksPerKey;
+      const int hgl = hg * kHeadsPerBlock + hh;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (hv) v = chunk < kCkvDim / 8 ? qn[chunk] : qr[chunk - kCkvDim / 8];
-      qf[kk] = v;
+      if (plan.active && hgl < a.heads)
+        v = c < 64 ? qn[(row * H + hgl) * 64 + c] : qr[(row * H + hgl) * 8 + (c - 64)];
+      *reinterpret_cast<uint4*>(&qs[hh * kQStride + c * 8]) = v;
     }
   }
+
+  const int32_t* topk = a.topk_dst + row * kTopK;
+  const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
+  const uint4* hbm_ckv = static_cast<const uint4*>(a.hbm_ckv);
+  const uint4* hbm_kpe = static_cast<const uint4*>(a.hbm_kpe);
+  const uint4* dram_ckv = static_cast<const uint4*>(a.dram_ckv);
+  const uint4* dram_kpe = static_cast<const uint4*>(a.dram_kpe);
+
+  // Resolve the keys of tiles first, first+splits, ... (kWindowTiles of
+  // them, one key per thread) into the window arrays.
+  auto resolve_window = [&](int first) {
+    const int w = tid / kTileKeys;
+    const int tile = first + w * splits;
+    const int j = tile * kTileKeys + (tid & (kTileKeys - 1));
+    int64_t src = -1, dst = -1;
+    int flag = 0;
+    if (tile < ntiles && j < list_len) {
+      const int slot = plan.active ? (j < plan.sparse ? topk[j] : plan.tail_start + (j - plan.sparse))
+                                   : a.copy_dst[b * a.copy_cap + j];
+      int64_t hrow = -1;
+      if (slot >= 0 && (slot >> kBlockShift) < a.hbm_cols) {
+        const int32_t blk = hbm_row_table[slot >> kBlockShift];
+        if (blk >= 0 && blk < a.hbm_blocks) hrow = static_cast<int64_t>(blk) * kBlock + (slot & (kBlock - 1));
+      }
+      if (plan.active && hrow >= 0 && slot < plan.lvis) {
+        flag = 1 | 4;
+        src = hrow;
+      }
+      if (FUSED && j < copy_count) {
+        const RowAddr ra = resolve_pair(a.copy_src[b * a.copy_cap + j], a.copy_dst[b * a.copy_cap + j],
+                                        a.dram_table + b * a.dram_cols, a.dram_cols, a.dram_blocks, hbm_row_table,
+                                        a.hbm_cols, a.hbm_blocks);
+        if (ra.src_row >= 0) {
+          flag |= 2 | 4;
+          src = ra.src_row;
+          dst = ra.dst_row;
+        }
+      }
+    }
+    win_src[tid] = src;
+    win_dst[tid] = dst;
+    win_flag[tid] = flag;
+  };
+  // Chunk c of the tile (c = j * 256 + tid, 72 chunks of 16 bytes per key):
+  // consecutive lanes read consecutive 16 bytes of one row, so a wave reads
+  // whole 1 KiB CKV rows (full-width PCIe requests for host rows).
+  auto load_tile = [&](int w, uint4 (&pf)[kChunksPerThread]) {
+#pragma unroll
+    for (int jj = 0; jj < kChunksPerThread; ++jj) {
+      const int cidx = jj * kAttnThreads + tid;
+      const int k = cidx / kChunksPerKey;
+      const int pc = cidx - k * kChunksPerKey;
+      const int wk = w * kTileKeys + k;
+      const int flag = win_flag[wk];
+      const int64_t src = win_src[wk];
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (flag & 4) {
+        const uint4* base = (FUSED && (flag & 2)) ? (pc < 64 ? dram_ckv + src * 64 : dram_kpe + src * 8)
+                                                  : (pc < 64 ? hbm_ckv + src * 64 : hbm_kpe + src * 8);
+        v = base[pc < 64 ? pc : pc - 64];
+      }
+      pf[jj] = v;
+    }
+  };
+  auto store_tile = [&](int w, const uint4 (&pf)[kChunksPerThread]) {
+#pragma unroll
+    for (int jj = 0; jj < kChunksPerThread; ++jj) {
+      const int cidx = jj * kAttnThreads + tid;
+      const int k = cidx / kChunksPerKey;
+      const int pc = cidx - k * kChunksPerKey;
+      *reinterpret_cast<uint4*>(&ks[k * kKStride + pc * 8]) = pf[jj];
+      if (FUSED) {
+        const int wk = w * kTileKeys + k;
+        if (win_flag[wk] & 2) {
+          const int64_t dst = win_dst[wk];
+          if (pc < 64)
+            static_cast<uint4*>(a.hbm_ckv)[dst * 64 + pc] = pf[jj];
+          else
+            static_cast<uint4*>(a.hbm_kpe)[dst * 8 + (pc - 64)] = pf[jj];
+        }
+      }
+    }
+  };
+
   const float qscale = a.scale * kLog2e;
   float m_run = -INFINITY;  // running max (base-2 logits) of head `head`
   float l_run = 0.f;        // this lane's share of the running sum
@@ -151,152 +249,101 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
 #pragma unroll
   for (int i = 0; i < kCkvDim / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int32_t* topk = a.topk_dst + row * kTopK;
-  const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
+  uint4 pf[kChunksPerThread];
+  for (int first = split; first < ntiles; first += kWindowTiles * splits) {
+    resolve_window(first);
+    __syncthreads();
+    const int wtiles = min(kWindowTiles, static_cast<int>(ceil_div(ntiles - first, splits)));
+    load_tile(0, pf);
+    for (int w = 0; w < wtiles; ++w) {
+      store_tile(w, pf);
+      __syncthreads();                     // tile w resident in LDS
+      if (w + 1 < wtiles) load_tile(w + 1, pf);  // in flight during the MFMA work below
 
-  for (int tile = split; tile < ntiles; tile += splits) {
-    const int kbase = tile * kTileKeys;
-    if (tid < kTileKeys) {
-      const int j = kbase + tid;
-      int kind = 0, use = 0;
-      int64_t src = -1, dst = -1;
-      if (j < list_len) {
-        int slot;
-        if (plan.active) {
-          slot = j < plan.sparse ? topk[j] : plan.tail_start + (j - plan.sparse);
-        } else {
-          slot = a.copy_dst[b * a.copy_cap + j];
+      if (wave_active && plan.active) {
+        // S^T tile: two 16-key blocks; lane holds S[head][kt*16 + 4g + i].
+        f32x4_t sacc[2];
+        const uint16_t* qrow = &qs[(wave * 16 + l16) * kQStride + g * 8];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          const uint16_t* krow = &ks[(kt * 16 + l16) * kKStride + g * 8];
+#pragma unroll
+          for (int kk = 0; kk < kQkDim / 32; ++kk) {
+            const uint4 kf = *reinterpret_cast<const uint4*>(krow + kk * 32);
+            const uint4 qf = *reinterpret_cast<const uint4*>(qrow + kk * 32);
+            acc = T::mfma16(__builtin_bit_cast(typename T::vec8, kf), __builtin_bit_cast(typename T::vec8, qf), acc);
+            if ((kk & 5) == 5) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
+          }
+          sacc[kt] = acc;
         }
-        int64_t hrow = -1;
-        if (slot >= 0 && (slot >> kBlockShift) < a.hbm_cols) {
-          const int32_t blk = hbm_row_table[slot >> kBlockShift];
-          if (blk >= 0 && blk < a.hbm_blocks) hrow = static_cast<int64_t>(blk) * kBlock + (slot & (kBlock - 1));
-        }
-        use = plan.active && hrow >= 0 && slot < plan.lvis;
-        if (use) {
-          kind = 1;
-          src = hrow;
-        }
-        if (FUSED && j < copy_count) {
-          const RowAddr ra =
-              resolve_pair(a.copy_src[b * a.copy_cap + j], a.copy_dst[b * a.copy_cap + j],
-                           a.dram_table + b * a.dram_cols, a.dram_cols, a.dram_blocks, hbm_row_table, a.hbm_cols,
-                           a.hbm_blocks);
-          if (ra.src_row >= 0) {
-            kind = 2;
-            src = ra.src_row;
-            dst = ra.dst_row;
+        float sv[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int k = kt * 16 + 4 * g + i;
+            const float x = (win_flag[w * kTileKeys + k] & 1) ? sacc[kt][i] * qscale : -INFINITY;
+            sv[kt * 4 + i] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        if (m_new != -INFINITY) {
+          const float alpha = exp2f(m_run - m_new);  // m_run == -inf gives 0
+          m_run = m_new;
+          float psum = 0.f;
+          float p[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            p[i] = exp2f(sv[i] - m_new);
+            psum += p[i];
+          }
+          l_run = l_run * alpha + psum;
+          // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
+          // ~16 mantissa bits of P instead of 8.
+          typename T::vec8 pb_hi, pb_lo;
+          uint16_t* phs = reinterpret_cast<uint16_t*>(&pb_hi);
+          uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            phs[i] = T::from_float(p[i]);
+            pls[i] = T::from_float(p[i] - T::to_float(phs[i]));
+          }
+          // A operand V^T[dim][key] read from the row-major tile: keys
+          // 4g..4g+3 and 16+4g..16+4g+3 (the lanes' S^T columns) at dim
+          // dt*16 + l16.
+          const uint16_t* v0 = &ks[(4 * g) * kKStride + l16];
+          const uint16_t* v1 = &ks[(16 + 4 * g) * kKStride + l16];
+#pragma unroll
+          for (int dt = 0; dt < kCkvDim / 16; ++dt) {
+            const int d = dt * 16;
+            const uint32_t x0 = v0[d] | (static_cast<uint32_t>(v0[kKStride + d]) << 16);
+            const uint32_t x1 = v0[2 * kKStride + d] | (static_cast<uint32_t>(v0[3 * kKStride + d]) << 16);
+            const uint32_t x2 = v1[d] | (static_cast<uint32_t>(v1[kKStride + d]) << 16);
+            const uint32_t x3 = v1[2 * kKStride + d] | (static_cast<uint32_t>(v1[3 * kKStride + d]) << 16);
+            const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(x0, x1, x2, x3));
+            f32x4_t acc = oacc[dt];
+            acc[0] *= alpha;
+            acc[1] *= alpha;
+            acc[2] *= alpha;
+            acc[3] *= alpha;
+            acc = T::mfma16(af, pb_hi, acc);
+            oacc[dt] = T::mfma16(af, pb_lo, acc);
+            if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
           }
         }
       }
-      key_kind[tid] = kind;
-      key_src[tid] = src;
-      key_dst[tid] = dst;
-      key_use[tid] = use;
+      __syncthreads();  // every wave is done with ks before the next store
     }
-    __syncthreads();
-    // Gather the tile: 32 keys x 72 chunks of 16 bytes.
-    for (int cidx = tid; cidx < kTileKeys * kChunksPerKey; cidx += kAttnThreads) {
-      const int k = cidx / kChunksPerKey;
-      const int part_i = cidx - k * kChunksPerKey;
-      const int kind = key_kind[k];
-      const int64_t src = key_src[k];
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (kind == 1) {
-        v = part_i < 64 ? static_cast<const uint4*>(a.hbm_ckv)[src * 64 + part_i]
-                        : static_cast<const uint4*>(a.hbm_kpe)[src * 8 + (part_i - 64)];
-      } else if (FUSED && kind == 2) {
-        v = part_i < 64 ? static_cast<const uint4*>(a.dram_ckv)[src * 64 + part_i]
-                        : static_cast<const uint4*>(a.dram_kpe)[src * 8 + (part_i - 64)];
-        const int64_t dst = key_dst[k];
-        if (part_i < 64)
-          static_cast<uint4*>(a.hbm_ckv)[dst * 64 + part_i] = v;
-        else
-          static_cast<uint4*>(a.hbm_kpe)[dst * 8 + (part_i - 64)] = v;
-      }
-      *reinterpret_cast<uint4*>(&ks[k * kKStride + part_i * 8]) = v;
-      if (part_i < 64) {
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
-#pragma unroll
-        for (int x = 0; x < 8; ++x) vt[(part_i * 8 + x) * kVStride + k] = e[x];
-      }
-    }
-    __syncthreads();
-
-    if (wave_active && plan.active) {
-      // S^T tile: two 16-key blocks; lane holds S[head][kt*16 + 4g + i].
-      f32x4_t sacc[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        const uint16_t* krow = &ks[(kt * 16 + l16) * kKStride + g * 8];
-#pragma unroll
-        for (int kk = 0; kk < kQkDim / 32; ++kk) {
-          const uint4 kf = *reinterpret_cast<const uint4*>(krow + kk * 32);
-          acc = T::mfma16(__builtin_bit_cast(typename T::vec8, kf), __builtin_bit_cast(typename T::vec8, qf[kk]),
-                          acc);
-        }
-        sacc[kt] = acc;
-      }
-      float sv[8];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int k = kt * 16 + 4 * g + i;
-          const float x = key_use[k] ? sacc[kt][i] * qscale : -INFINITY;
-          sv[kt * 4 + i] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      if (m_new != -INFINITY) {
-        const float alpha = exp2f(m_run - m_new);  // m_run == -inf gives 0
-        m_run = m_new;
-        float psum = 0.f;
-        float p[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          p[i] = exp2f(sv[i] - m_new);
-          psum += p[i];
-        }
-        l_run = l_run * alpha + psum;
-        // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
-        // ~16 mantissa bits of P instead of 8.
-        typename T::vec8 pb_hi, pb_lo;
-        uint16_t* phs = reinterpret_cast<uint16_t*>(&pb_hi);
-        uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          phs[i] = T::from_float(p[i]);
-          pls[i] = T::from_float(p[i] - T::to_float(phs[i]));
-        }
-#pragma unroll
-        for (int dt = 0; dt < kCkvDim / 16; ++dt) {
-          const uint16_t* vrow = &vt[(dt * 16 + l16) * kVStride];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * g);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * g);
-          const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-          f32x4_t acc = oacc[dt];
-          acc[0] *= alpha;
-          acc[1] *= alpha;
-          acc[2] *= alpha;
-          acc[3] *= alpha;
-          acc = T::mfma16(af, pb_hi, acc);
-          oacc[dt] = T::mfma16(af, pb_lo, acc);
-        }
-      }
-    }
-    __syncthreads();
   }
 
   // Split partials: max, sum and un-normalised numerator per head.
   if (!wave_active || head >= a.heads) return;
   float lsum = l_run + __shfl_xor(l_run, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
-  const int64_t pidx = (row * splits + split) * H + head;
   if (g == 0) {
     part.ml[pidx * 2 + 0] = m_run;
     part.ml[pidx * 2 + 1] = lsum;

@@ -154,6 +154,12 @@ def make_chain_case(
         return index_table[b, t // BLOCK].long() * BLOCK + (t % BLOCK)
 
     def scores_of(b: int, phys: torch.Tensor):
+        if not guard:
+            # unguarded (benchmark) inputs: float32 scores are enough to place the pool
+            k32 = kc[phys].float()
+            s = [(torch.relu(k32 @ q_index[b * Q + q].float().T) @ weights[b * Q + q].float()).double().numpy()
+                 for q in range(Q)]
+            return np.stack(s), np.zeros((Q, phys.numel()))
         k = _f64(kc[phys])
         s, e = [], []
         for q in range(Q):
@@ -161,7 +167,10 @@ def make_chain_case(
             ww = _f64(weights[b * Q + q])
             dots = k @ qq.T
             s.append(np.maximum(dots, 0.0) @ ww)
-            e.append(_ERR_UNIT * (np.abs(k) @ np.abs(qq).T) @ np.abs(ww))
+            if guard:
+                e.append(_ERR_UNIT * (np.abs(k) @ np.abs(qq).T) @ np.abs(ww))
+            else:
+                e.append(np.zeros_like(s[-1]))
         return np.stack(s), np.stack(e)
 
     pool_rows = B + extra_pool_rows
@@ -353,3 +362,76 @@ def baseline_config(index: int, seed: int = 0, dtype: torch.dtype = torch.bfloat
         tails = rng.integers(4, 128, size=16)
         return make_chain_case(16, 49152, 8192, tails, seed=seed, dtype=dtype, guard=guard, mtp=True)
     raise ValueError(f"no baseline config {index}")
+
+
+def _torch_scores(keys: torch.Tensor, q: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return torch.relu(keys @ q.T) @ w
+
+
+def make_drift_case(
+    batch: int,
+    source_lens,
+    cache_tokens,
+    tails,
+    *,
+    miss_frac=(0.05, 0.15),
+    seed: int = 0,
+    dtype: torch.dtype = torch.bfloat16,
+    index_heads: int = 32,
+    attn_heads: int = 64,
+    calib_device=None,
+) -> ChainCase:
+    """Steady-state decode workload for benchmarking.
+
+    Adds a second index query ``query_index_b`` per request, a perturbation
+    of ``query_index`` calibrated (bisection on the perturbation size) so
+    that its top-2048 set differs from the first query's by the request's
+    target miss fraction drawn from ``miss_frac``.  The pool starts with the
+    first query's top-C cached; alternating the two queries step after step
+    then makes every step miss ~that fraction, with the HBM cache kept
+    consistent by the copies themselves -- no state restore between steps.
+    """
+    case = make_chain_case(batch, source_lens, cache_tokens, tails, miss_frac=(0.0, 0.0), seed=seed, dtype=dtype,
+                           guard=False, index_heads=index_heads, attn_heads=attn_heads)
+    t = case.tensors
+    B = case.meta["batch"]
+    rng = np.random.default_rng(seed + 7)
+    g = torch.Generator().manual_seed(seed + 7)
+    dev = torch.device(calib_device) if calib_device is not None else torch.device("cpu")
+    kc = t["index_key_cache"].view(-1, IDX).to(dev).float()
+    qa = t["query_index"].to(dev).float()
+    w = t["index_weights"].to(dev).float()
+    table = t["index_block_table"].to(dev)
+    qb = torch.empty_like(t["query_index"])
+    achieved = []
+    for b in range(B):
+        n = case.meta["source_lens"][b]
+        if n <= TOPK or case.meta["cache_tokens"][b] < TOPK:
+            qb[b] = t["query_index"][b]
+            achieved.append(0.0)
+            continue
+        tok = torch.arange(n, device=dev)
+        keys = kc[table[b, tok // BLOCK].long() * BLOCK + tok % BLOCK]
+        top_a = torch.topk(_torch_scores(keys, qa[b], w[b]), TOPK).indices
+        in_a = torch.zeros(n, dtype=torch.bool, device=dev)
+        in_a[top_a] = True
+        eps = torch.randn(qa[b].shape, generator=g).to(dev)
+        target = rng.uniform(*miss_frac)
+        lo, hi = 0.0, 2.0
+        best = (1.0, qa[b].to(dtype), 0.0)
+        for _ in range(14):
+            mid = 0.5 * (lo + hi)
+            cand = (qa[b] + mid * eps).to(dtype)
+            top_b = torch.topk(_torch_scores(keys, cand.float(), w[b]), TOPK).indices
+            frac = float((~in_a[top_b]).sum()) / TOPK
+            if abs(frac - target) < abs(best[0] - target):
+                best = (frac, cand, mid)
+            if frac < target:
+                lo = mid
+            else:
+                hi = mid
+        qb[b] = best[1].cpu()
+        achieved.append(best[0])
+    t["query_index_b"] = qb
+    case.meta["drift_miss_frac"] = achieved
+    return case
