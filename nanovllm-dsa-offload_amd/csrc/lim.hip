@@ -45,6 +45,7 @@ constexpr int kManageThreads = 512;
 constexpr int kBins = 2048;                       // radix histogram bins (11 bits)
 constexpr int kBinsPerThread = kBins / kManageThreads;
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
+constexpr int kLdsSlots = 4096;  // cache budgets up to this keep their slot tables in LDS
 constexpr uint32_t kStateShift = 24;
 constexpr uint32_t kStateFree = 0;
 constexpr uint32_t kStateHit = 1;
@@ -584,6 +585,8 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kTopK];
+  __shared__ uint32_t lds_stab[kLdsSlots];
+  __shared__ uint32_t lds_skey[kLdsSlots];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int n = a.num_candidates[b];
@@ -596,28 +599,47 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + static_cast<int64_t>(b) * cap;
   int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kSlotStride;
-  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kSlotStride;
+  // Slot tables: LDS for budgets up to kLdsSlots, else the workspace.
+  const bool lds_tables = c <= kLdsSlots;
+  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kSlotStride;
+  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kSlotStride;
   int32_t* misses = w.miss_list + static_cast<int64_t>(b) * kUnionCap;
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   int eq_run = 0, miss_run = 0;
   if constexpr (RES > 0) {
+    // Scores and pool slots of all the request's tokens, loaded once.  A
+    // slot is kept as 16 bits: 0 <= slot < C (C <= 16383) or 0xffff for
+    // "not cached", which is all the ordered pass distinguishes.
     uint32_t u[RES][kItems];
-    uint32_t lo = 0xffffffffu, hi = 0u;
+    uint32_t pk[RES][kItems / 2];
+    auto p16 = [c](int32_t v) -> uint32_t { return (v >= 0 && v < c) ? static_cast<uint32_t>(v) : 0xffffu; };
 #pragma unroll
     for (int ch = 0; ch < RES; ++ch) {
       const int t0 = ch * kChunk + tid * kItems;
       if (t0 + kItems <= n) {
         const float4 x = *reinterpret_cast<const float4*>(s + t0);
         const float4 y = *reinterpret_cast<const float4*>(s + t0 + 4);
+        const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
+        const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
         u[ch][0] = score_key(x.x); u[ch][1] = score_key(x.y); u[ch][2] = score_key(x.z); u[ch][3] = score_key(x.w);
         u[ch][4] = score_key(y.x); u[ch][5] = score_key(y.y); u[ch][6] = score_key(y.z); u[ch][7] = score_key(y.w);
+        pk[ch][0] = p16(pa.x) | (p16(pa.y) << 16);
+        pk[ch][1] = p16(pa.z) | (p16(pa.w) << 16);
+        pk[ch][2] = p16(pb.x) | (p16(pb.y) << 16);
+        pk[ch][3] = p16(pb.z) | (p16(pb.w) << 16);
       } else {
 #pragma unroll
         for (int e = 0; e < kItems; ++e) u[ch][e] = t0 + e < n ? score_key(s[t0 + e]) : 0u;
+#pragma unroll
+        for (int e = 0; e < kItems / 2; ++e) {
+          const uint32_t v0 = t0 + 2 * e < n ? p16(pool[t0 + 2 * e]) : 0xffffu;
+          const uint32_t v1 = t0 + 2 * e + 1 < n ? p16(pool[t0 + 2 * e + 1]) : 0xffffu;
+          pk[ch][e] = v0 | (v1 << 16);
+        }
       }
     }
+    uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
     for (int ch = 0; ch < RES; ++ch)
 #pragma unroll
@@ -638,16 +660,16 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
         },
         hist, scratch, bcast);
     const bool need_rank = sel.cnt_eq != sel.need_eq;
-    int32_t nxt[kItems];
-    load_pool8(pool, n, tid * kItems, nxt);
 #pragma unroll
     for (int ch = 0; ch < RES; ++ch) {
       const int base = ch * kChunk;
       if (base >= n) break;  // uniform
       int32_t slot[kItems];
 #pragma unroll
-      for (int e = 0; e < kItems; ++e) slot[e] = nxt[e];
-      if (ch + 1 < RES && base + kChunk < n) load_pool8(pool, n, base + kChunk + tid * kItems, nxt);
+      for (int e = 0; e < kItems; ++e) {
+        const uint32_t v = (pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        slot[e] = v == 0xffffu ? -1 : static_cast<int32_t>(v);
+      }
       const int t0 = base + tid * kItems;
       bool in[kItems];
 #pragma unroll
@@ -695,6 +717,8 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kUnionCap];
+  __shared__ uint32_t lds_stab[kLdsSlots];
+  __shared__ uint32_t lds_skey[kLdsSlots];
   __shared__ uint32_t thr[kMtpQueries];
   __shared__ int need[kMtpQueries];
   __shared__ int rank_needed[kMtpQueries];
@@ -710,8 +734,9 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + static_cast<int64_t>(b) * kMtpQueries * cap;
   int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kSlotStride;
-  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kSlotStride;
+  const bool lds_tables = c <= kLdsSlots;
+  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kSlotStride;
+  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kSlotStride;
   uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
   int32_t* miss_src = a.miss_src + static_cast<int64_t>(b) * kUnionCap;
   int32_t* miss_dst = a.miss_dst + static_cast<int64_t>(b) * kUnionCap;

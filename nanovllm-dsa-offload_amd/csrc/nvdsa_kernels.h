@@ -103,6 +103,7 @@ struct SfaArgs {
   const void* dram_ckv;
   int64_t dram_cols;
   int64_t dram_blocks;
+  int miss_splits;              // fused: splits per row reserved for the miss tiles (set by the launcher)
   void* workspace;
   size_t workspace_bytes;
 };

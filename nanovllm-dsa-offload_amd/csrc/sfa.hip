@@ -135,8 +135,28 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   const int list_len = plan.active ? plan.count : (FUSED ? copy_count : 0);
   const int ntiles = static_cast<int>(ceil_div(list_len, kTileKeys));
   const int64_t pidx = (row * splits + split) * H + head;
+  // Tiles of this split: t_first, t_first + t_stride, ... < t_end.  Fused:
+  // splits [0, miss_splits) take the tiles holding host-sourced misses (the
+  // first ceil(copy_count/32) tiles), the others the HBM-only tiles, so the
+  // host-link-bound copies and the HBM-bound tiles proceed side by side
+  // instead of every workgroup first stalling on its share of the copy.
+  int t_first = split, t_stride = splits, t_end = ntiles;
+  if (FUSED) {
+    const int miss_splits = a.miss_splits;
+    const int mtiles = static_cast<int>(ceil_div(copy_count, kTileKeys));
+    if (split < miss_splits) {
+      t_first = split;
+      t_stride = miss_splits;
+      t_end = mtiles < ntiles ? mtiles : ntiles;
+    } else {
+      t_first = mtiles + (split - miss_splits);
+      t_stride = splits - miss_splits;
+      t_end = ntiles;
+    }
+  }
+  const int my_tiles = t_first < t_end ? static_cast<int>(ceil_div(t_end - t_first, t_stride)) : 0;
 
-  if (split >= ntiles) {  // nothing for this split (whole workgroup)
+  if (my_tiles == 0) {  // nothing for this split (whole workgroup)
     if (wave_active && head < a.heads && g == 0) {
       part.ml[pidx * 2 + 0] = -INFINITY;
       part.ml[pidx * 2 + 1] = 0.f;
@@ -170,11 +190,12 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   // them, one key per thread) into the window arrays.
   auto resolve_window = [&](int first) {
     const int w = tid / kTileKeys;
-    const int tile = first + w * splits;
+    const int idx = first + w;  // position in this split's tile sequence
+    const int tile = t_first + idx * t_stride;
     const int j = tile * kTileKeys + (tid & (kTileKeys - 1));
     int64_t src = -1, dst = -1;
     int flag = 0;
-    if (tile < ntiles && j < list_len) {
+    if (idx < my_tiles && j < list_len) {
       const int slot = plan.active ? (j < plan.sparse ? topk[j] : plan.tail_start + (j - plan.sparse))
                                    : a.copy_dst[b * a.copy_cap + j];
       int64_t hrow = -1;
@@ -250,10 +271,10 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   for (int i = 0; i < kCkvDim / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   uint4 pf[kChunksPerThread];
-  for (int first = split; first < ntiles; first += kWindowTiles * splits) {
+  for (int first = 0; first < my_tiles; first += kWindowTiles) {
     resolve_window(first);
     __syncthreads();
-    const int wtiles = min(kWindowTiles, static_cast<int>(ceil_div(ntiles - first, splits)));
+    const int wtiles = min(kWindowTiles, my_tiles - first);
     load_tile(0, pf);
     for (int w = 0; w < wtiles; ++w) {
       store_tile(w, pf);
@@ -302,6 +323,9 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
             psum += p[i];
           }
           l_run = l_run * alpha + psum;
+          // The numerator needs rescaling only when some head's running max
+          // moved in this tile (alpha == 1 exactly otherwise).
+          const bool rescale = __any(alpha != 1.f);
           // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
           // ~16 mantissa bits of P instead of 8.
           typename T::vec8 pb_hi, pb_lo;
@@ -326,10 +350,12 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
             const uint32_t x3 = v1[2 * kKStride + d] | (static_cast<uint32_t>(v1[3 * kKStride + d]) << 16);
             const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(x0, x1, x2, x3));
             f32x4_t acc = oacc[dt];
-            acc[0] *= alpha;
-            acc[1] *= alpha;
-            acc[2] *= alpha;
-            acc[3] *= alpha;
+            if (rescale) {
+              acc[0] *= alpha;
+              acc[1] *= alpha;
+              acc[2] *= alpha;
+              acc[3] *= alpha;
+            }
             acc = T::mfma16(af, pb_hi, acc);
             oacc[dt] = T::mfma16(af, pb_lo, acc);
             if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
@@ -399,10 +425,14 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
   const int splits = choose_splits(rows, hgroups);
+  SfaArgs args = a;
+  // Fused: ~30% of a row's splits handle the host-sourced miss tiles.
+  args.miss_splits = FUSED ? (splits >= 2 ? static_cast<int>((splits * 3 + 9) / 10) : 0) : 0;
+  if (FUSED && args.miss_splits >= splits) args.miss_splits = splits - 1;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
   prof_before(stream, FUSED ? kKernSfaSplitFused : kKernSfaSplit);
   hipLaunchKernelGGL((sfa_split_kernel<T, FUSED>), dim3(static_cast<uint32_t>(rows * splits), hgroups),
-                     dim3(kAttnThreads), 0, stream, a, p, splits);
+                     dim3(kAttnThreads), 0, stream, args, p, splits);
   prof_after(stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
