@@ -16,6 +16,13 @@ the miss copy and the CPU oracle on the same inputs are reported alongside.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 Prints one JSON line.
+
+Two helper modes serve the hardware-counter runs whose summaries sit in
+profiles/: ``--kernels-only {lim,fused,split,sfa,copy} [--reps R]`` launches
+one kernel family alone on the same cfg1 inputs (``copy`` is the calibration
+kernel: torch.mul over 256 MiB of float32), for ``rocprofv3 --pmc``; and
+``--summarize-pmc DIR`` reduces the counter CSVs under DIR to per-kernel mean
+values (DIR/pmc_summary.csv).
 """
 
 from __future__ import annotations
@@ -52,7 +59,66 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-steps", type=int, default=8, help="layer-steps of the CPU oracle sample")
+    p.add_argument("--kernels-only", choices=("lim", "fused", "split", "sfa", "copy"), default=None,
+                   help="launch one kernel family alone (for rocprofv3 --pmc) and exit")
+    p.add_argument("--reps", type=int, default=4, help="launches in --kernels-only mode")
+    p.add_argument("--summarize-pmc", default=None, metavar="DIR",
+                   help="reduce rocprofv3 counter CSVs under DIR to DIR/pmc_summary.csv and exit")
     return p.parse_args()
+
+
+# ---- hardware-counter helpers ------------------------------------------------
+PMC_KERNELS = ("lim_score_kernel", "lim_manage_mtp_kernel", "lim_manage_kernel", "sfa_split_kernel",
+               "sfa_combine_kernel", "scatter_copy_kernel")
+PMC_PROFILE = REPO / "profiles" / "lim_score_cfg1_pmc.txt"
+
+
+def summarize_pmc(root: str) -> int:
+    """Mean counter value per (run, kernel, counter) over every
+    ``*counter_collection.csv`` one level below ``root``; the raw CSVs are
+    deleted afterwards (they run to tens of MB)."""
+    import collections
+    import csv
+    import glob
+    import re
+
+    pat = re.compile("(" + "|".join(PMC_KERNELS) + r")(<[^>]*>)?")
+    out = []
+    for path in sorted(glob.glob(os.path.join(root, "*", "*counter_collection.csv"))):
+        agg = collections.defaultdict(lambda: collections.defaultdict(list))
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                name = row.get("Kernel_Name", "")
+                m = pat.search(name)
+                if m:
+                    short = m.group(0)
+                elif "MulFunctor<float>" in name:
+                    short = "calib_mul_f32"
+                else:
+                    continue
+                agg[short][row["Counter_Name"]].append(float(row["Counter_Value"]))
+        run = os.path.basename(os.path.dirname(path))
+        for kern, counters in agg.items():
+            for cn, vals in counters.items():
+                out.append(f"{run},{kern},{cn},{len(vals)},{sum(vals) / len(vals):.6g}")
+        os.remove(path)
+    with open(os.path.join(root, "pmc_summary.csv"), "w") as f:
+        f.write("run,kernel,counter,dispatches,mean_value\n" + "\n".join(out) + "\n")
+    print("\n".join(out), flush=True)
+    return 0
+
+
+def pmc_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (lines ``traffic_bytes_per_launch <kernel> <bytes>``), or None."""
+    import re
+
+    try:
+        text = PMC_PROFILE.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\s+" + re.escape(kernel) + r"\s+(\d+)\s*$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def measure_h2d_peak(torch, dev) -> float:
@@ -93,6 +159,8 @@ def measure_hbm_copy(torch, dev) -> float:
 
 def main() -> int:
     args = parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(args.summarize_pmc)
     if args.gpus != 1:
         log(f"bench.py measures one GPU only (got --gpus {args.gpus}): every box of this build has a single "
             "MI355X; the multi-GPU sharding of this path is described in DESIGN.md, not benchmarked.")
@@ -107,6 +175,15 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.kernels_only == "copy":
+        n = 64 << 20  # float32 elements: 256 MiB read and 256 MiB written per launch
+        a = torch.ones(n, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(args.reps):
+            torch.mul(a, 1.5, out=b)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copy done, {args.reps} launches of {4 * n} bytes each way")
+        return 0
     rng = np.random.default_rng(1001)
     B, N, C = 24, 32768, 2048
     tails = rng.integers(1, 128, size=B)
@@ -152,6 +229,24 @@ def main() -> int:
         lim(i)
         scatter()
         sfa()
+
+    if args.kernels_only:
+        lim(0)
+        fused()
+        torch.cuda.synchronize()
+        for i in range(args.reps):
+            if args.kernels_only == "lim":
+                lim(i + 1)
+            elif args.kernels_only == "fused":
+                fuse_step(i + 1)
+            elif args.kernels_only == "split":
+                split_step(i + 1)
+            else:
+                sfa()
+        torch.cuda.synchronize()
+        log(f"bench: kernels-only {args.kernels_only} done, {args.reps} launches, "
+            f"last misses {int(t['miss_counts'].sum())}")
+        return 0
 
     miss_log = torch.zeros(args.steps, B, dtype=torch.int32, device=dev)
 
@@ -271,7 +366,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "kernel": "lim_score_kernel", "achieved": round(score_ach, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(score_ach / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(score_ach / HBM_PEAK_GBS, 4), "traffic": pmc_traffic("lim_score_kernel"),
             "algorithmic_bytes": score_bytes, "mean_us": round(k["lim_score_kernel"] * 1000, 2),
         },
         "h2d": {

@@ -962,29 +962,23 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   const LimWs w = carve(a.workspace, a.batch, a.source_capacity, Q);
   const dim3 grid(static_cast<uint32_t>(ceil_div(a.cols, kScoreWaves)), static_cast<uint32_t>(a.batch));
   const int mtp = Q > 1 ? 1 : 0;
-  prof_before(stream, kKernLimScore);
   if (a.heads == 32) {
-    hipLaunchKernelGGL((lim_score_kernel<T, 32, Q>), grid, dim3(kScoreWaves * kWave), 0, stream, a, w.scores, mtp);
+    launch_kernel(kKernLimScore, lim_score_kernel<T, 32, Q>, grid, dim3(kScoreWaves * kWave), stream, a, w.scores,
+                  mtp);
   } else {
-    hipLaunchKernelGGL((lim_score_kernel<T, 64, Q>), grid, dim3(kScoreWaves * kWave), 0, stream, a, w.scores, mtp);
+    launch_kernel(kKernLimScore, lim_score_kernel<T, 64, Q>, grid, dim3(kScoreWaves * kWave), stream, a, w.scores,
+                  mtp);
   }
-  prof_after(stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (Q == 1) {
-    prof_before(stream, kKernLimManage);
-    const dim3 grid(static_cast<uint32_t>(a.batch)), block(kManageThreads);
-    if (a.source_capacity <= 8 * kChunk) {
-      hipLaunchKernelGGL(lim_manage_kernel<8>, grid, block, 0, stream, a, w);
-    } else {
-      hipLaunchKernelGGL(lim_manage_kernel<0>, grid, block, 0, stream, a, w);
-    }
+  const dim3 mgrid(static_cast<uint32_t>(a.batch)), mblock(kManageThreads);
+  if (Q > 1) {
+    launch_kernel(kKernLimManageMtp, lim_manage_mtp_kernel, mgrid, mblock, stream, a, w);
+  } else if (a.source_capacity <= 8 * kChunk) {
+    launch_kernel(kKernLimManage, lim_manage_kernel<8>, mgrid, mblock, stream, a, w);
   } else {
-    prof_before(stream, kKernLimManageMtp);
-    hipLaunchKernelGGL(lim_manage_mtp_kernel, dim3(static_cast<uint32_t>(a.batch)), dim3(kManageThreads), 0,
-                       stream, a, w);
+    launch_kernel(kKernLimManage, lim_manage_kernel<0>, mgrid, mblock, stream, a, w);
   }
-  prof_after(stream);
   return hipGetLastError();
 }
 

@@ -113,18 +113,15 @@ constexpr int64_t kMaxGridThreads = (int64_t{1} << 31);
 
 namespace nvdsa {
 
-void prof_before(hipStream_t stream, int kernel_id) {
+ProfEvents prof_events(int kernel_id) {
   ProfState& p = g_prof;
-  if (!p.on || p.count >= p.capacity) return;
-  (void)hipEventRecord(p.events[2 * p.count], stream);
+  ProfEvents ev;
+  if (!p.on || p.count >= p.capacity) return ev;
+  ev.start = p.events[2 * p.count];
+  ev.stop = p.events[2 * p.count + 1];
   p.ids[p.count] = kernel_id;
-}
-
-void prof_after(hipStream_t stream) {
-  ProfState& p = g_prof;
-  if (!p.on || p.count >= p.capacity) return;
-  (void)hipEventRecord(p.events[2 * p.count + 1], stream);
   ++p.count;
+  return ev;
 }
 
 }  // namespace nvdsa

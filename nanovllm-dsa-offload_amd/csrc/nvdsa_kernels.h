@@ -2,6 +2,7 @@
 // kernel translation units.  Arguments are already validated by the caller.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -21,10 +22,26 @@ enum KernelId : int {
   kKernSfaCombine = 6,
   kKernCount = 7
 };
-// Bracket one kernel launch with timing events when instrumentation is on
-// for the calling thread (no-ops otherwise).
-void prof_before(hipStream_t stream, int kernel_id);
-void prof_after(hipStream_t stream);
+// Timing events for the next launch of `kernel_id` when instrumentation is
+// on for the calling thread (nvdsa_profile_begin); both null otherwise.
+struct ProfEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+ProfEvents prof_events(int kernel_id);
+
+// Launch `kernel` on `stream`.  When timed, the events ride on the kernel's
+// own dispatch (hipExtLaunchKernelGGL), so the recorded interval is the
+// kernel's execution alone, without the gaps of separate event records.
+template <typename F, typename... Args>
+inline void launch_kernel(int kernel_id, F kernel, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+  const ProfEvents ev = prof_events(kernel_id);
+  if (ev.start != nullptr) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, ev.start, ev.stop, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+  }
+}
 
 // ---- scatter_copy --------------------------------------------------------
 struct ScatterArgs {

@@ -71,10 +71,8 @@ hipError_t launch_scatter_copy(const ScatterArgs& a, hipStream_t stream) {
   if (a.batch == 0) return hipSuccess;
   const int64_t chunks = ceil_div(a.cap, kRowsPerBlock);
   const int64_t blocks = a.batch * chunks;
-  prof_before(stream, kKernScatter);
-  hipLaunchKernelGGL(scatter_copy_kernel, dim3(static_cast<uint32_t>(blocks)),
-                     dim3(kWavesPerBlock * kWave), 0, stream, a, chunks);
-  prof_after(stream);
+  launch_kernel(kKernScatter, scatter_copy_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kWavesPerBlock * kWave),
+                stream, a, chunks);
   return hipGetLastError();
 }
 

@@ -430,16 +430,13 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   args.miss_splits = FUSED ? (splits >= 2 ? static_cast<int>((splits * 3 + 9) / 10) : 0) : 0;
   if (FUSED && args.miss_splits >= splits) args.miss_splits = splits - 1;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
-  prof_before(stream, FUSED ? kKernSfaSplitFused : kKernSfaSplit);
-  hipLaunchKernelGGL((sfa_split_kernel<T, FUSED>), dim3(static_cast<uint32_t>(rows * splits), hgroups),
-                     dim3(kAttnThreads), 0, stream, args, p, splits);
-  prof_after(stream);
+  launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED>,
+                dim3(static_cast<uint32_t>(rows * splits), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads),
+                stream, args, p, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  prof_before(stream, kKernSfaCombine);
-  hipLaunchKernelGGL((sfa_combine_kernel<T>), dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads)),
-                     dim3(128), 0, stream, a, p, splits);
-  prof_after(stream);
+  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>,
+                dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads)), dim3(128), stream, a, p, splits);
   return hipGetLastError();
 }
 
