@@ -213,8 +213,9 @@ __device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
     red[2 * nw + 1] = h;
   }
   __syncthreads();
-  lo = red[2 * nw];
-  hi = red[2 * nw + 1];
+  // Uniform values (readfirstlane): they steer loops that contain barriers.
+  lo = __builtin_amdgcn_readfirstlane(red[2 * nw]);
+  hi = __builtin_amdgcn_readfirstlane(red[2 * nw + 1]);
   __syncthreads();
 }
 
@@ -265,10 +266,10 @@ __device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Vis
       acc += cnt[j];
     }
     __syncthreads();
-    prefix |= static_cast<uint32_t>(bcast[0]) << lo;
+    prefix |= static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bcast[0])) << lo;
     pmask |= dmask << lo;
-    remaining -= bcast[1];
-    cnt_eq = bcast[2];
+    remaining -= __builtin_amdgcn_readfirstlane(bcast[1]);
+    cnt_eq = __builtin_amdgcn_readfirstlane(bcast[2]);
     __syncthreads();
   }
   return SelectOut{prefix + kmin, remaining, cnt_eq};
@@ -326,7 +327,9 @@ __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, 
   }
   __syncthreads();
   const uint64_t excl = scratch[wid] + x - v;
-  *total = scratch[nw];
+  const uint64_t t = scratch[nw];
+  *total = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t >> 32))) << 32) |
+           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t)));
   __syncthreads();
   return excl;
 }

@@ -106,7 +106,7 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
   }
   __syncthreads();
   int excl = scratch[wid] + x - v;
-  *total = scratch[nw];
+  *total = __builtin_amdgcn_readfirstlane(scratch[nw]);  // uniform: may steer barrier-containing code
   __syncthreads();
   return excl;
 }
