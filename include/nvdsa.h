@@ -140,7 +140,9 @@ int nvdsa_scatter_copy(const nvdsa_tensor* src_ids,
 /* Absorbed-MLA decode attention over top-2048 slots + dense tail.
  * Replaces torch.ops.nanovllm_dsa.sparse_tail_attention
  * (reference: bindings/nanovllm_ops.cpp:664-669,
- *  checks: ops/sparse_tail_attention/sparse_tail_attention_torch_adpt.h:17-88). */
+ *  checks: ops/sparse_tail_attention/sparse_tail_attention_torch_adpt.h:17-88).
+ * The workspace (this size) serves the four attention entry points; calls
+ * that may run concurrently need separate workspaces. */
 size_t nvdsa_sparse_tail_attention_workspace_size(int64_t query_rows,
                                                   int64_t heads,
                                                   int64_t max_kv_tokens);
@@ -224,6 +226,57 @@ int nvdsa_fused_copy_sfa_mtp(const nvdsa_tensor* query_rope,
                              const nvdsa_tensor* attention_out,
                              void* workspace, size_t workspace_bytes,
                              void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* First-decode LIDU initialisation of one request (replaces the reference's
+ * PyTorch slow path initialize_lidu_row, nanovllm/models/dsa_offload_ops.py:251-360,
+ * which the model calls eagerly before the first stable decode step,
+ * nanovllm/models/glm_mla.py:1260-1286).  Scores without ReLU
+ * (s[t] = sum_h w[h] * q[h].k[t]), the cache_tokens largest over tokens
+ * [0, candidate_len) (ties to the lower token), slot i to the i-th smallest
+ * selected token (the reference's order is that of torch.topk(sorted=False)),
+ * every other entry of the pool row set to -1, and the selected rows copied
+ * DRAM -> HBM.  query [H, 128] (or [1, H, 128]), weights [H]; caches in the
+ * 3-D views scatter_copy takes; table arguments are 1-D rows.  cache_tokens
+ * <= 0 is a no-op; the reference's ValueErrors (cache_tokens < 2048,
+ * candidate_len < cache_tokens, incomplete blocks) return NVDSA_ERR_ARG with
+ * its message.  Enqueues on `stream` without synchronising. */
+size_t nvdsa_initialize_lidu_row_workspace_size(int64_t source_capacity);
+
+int nvdsa_initialize_lidu_row(const nvdsa_tensor* query,
+                              const nvdsa_tensor* weights,
+                              const nvdsa_tensor* index_cache,
+                              const nvdsa_tensor* index_block_table,
+                              int64_t candidate_len,
+                              int64_t cache_tokens,
+                              const nvdsa_tensor* cache_slots_row,
+                              const nvdsa_tensor* hbm_kpe,
+                              const nvdsa_tensor* hbm_ckv,
+                              const nvdsa_tensor* dram_kpe,
+                              const nvdsa_tensor* dram_ckv,
+                              const nvdsa_tensor* hbm_block_table,
+                              const nvdsa_tensor* dram_block_table,
+                              int64_t block_size,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* IndexShare shared layer (replaces initialize_lidu_row_shared,
+ * nanovllm/models/dsa_offload_ops.py:363-411): copy this layer's DRAM rows of
+ * every token the owner's pool row caches, ascending token, to its slot.  Like
+ * the reference (whose nonzero() synchronises), it waits for `stream` once to
+ * compare the cached count with cache_tokens before the copy, and returns
+ * NVDSA_ERR_RUNTIME with the reference's message when they differ.  Takes the
+ * workspace size of nvdsa_initialize_lidu_row. */
+int nvdsa_initialize_lidu_row_shared(const nvdsa_tensor* cache_slots_row,
+                                     int64_t cache_tokens,
+                                     const nvdsa_tensor* hbm_kpe,
+                                     const nvdsa_tensor* hbm_ckv,
+                                     const nvdsa_tensor* dram_kpe,
+                                     const nvdsa_tensor* dram_ckv,
+                                     const nvdsa_tensor* hbm_block_table,
+                                     const nvdsa_tensor* dram_block_table,
+                                     void* workspace, size_t workspace_bytes,
+                                     void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Pinned, device-mapped host memory for the DRAM KV caches: the counterpart

@@ -42,7 +42,8 @@ namespace {
 constexpr int kScoreWaves = 4;                  // waves per score workgroup
 constexpr int kQStride = kIndexDim + 8;         // padded LDS row (bank spread)
 constexpr int kManageThreads = 512;
-constexpr int kBins = 2048;                       // radix histogram bins (11 bits)
+constexpr int kDigitBits = 13;                    // radix digit width
+constexpr int kBins = 1 << kDigitBits;            // radix histogram bins
 constexpr int kBinsPerThread = kBins / kManageThreads;
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr int kLdsSlots = 4096;  // cache budgets up to this keep their slot tables in LDS
@@ -92,17 +93,24 @@ __device__ inline bool lim_mtp_row_valid(int n, int c, int r, int64_t cap, int64
 
 // ---------------------------------------------------------------------------
 // 1. Scores.
-template <typename T, int HEADS, int Q>
-__global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs a, float* scores, int mtp) {
+// RELU = false is the first-decode initialisation score (no ReLU,
+// nanovllm/models/dsa_offload_ops.py:306-311); there `fixed_n` >= 0 gives the
+// candidate count of the single request and the row guards do not apply.
+template <typename T, int HEADS, int Q, bool RELU>
+__global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs a, float* scores, int mtp,
+                                                                        int fixed_n) {
   __shared__ uint16_t qs[Q * HEADS * kQStride];
   __shared__ float ws[Q * HEADS];
   const int b = blockIdx.y;
-  const int n = a.num_candidates[b];
-  const int c = a.num_cache[b];
-  const int r = a.pool_entries[b];
-  const bool valid = mtp ? lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)
-                         : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
-  if (!valid) return;
+  int n = fixed_n;
+  if (fixed_n < 0) {
+    n = a.num_candidates[b];
+    const int c = a.num_cache[b];
+    const int r = a.pool_entries[b];
+    const bool valid = mtp ? lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)
+                           : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
+    if (!valid) return;
+  }
   const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kScoreWaves;
   if (col0 * kBlock >= n) return;
 
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
           acc = T::mfma32(__builtin_bit_cast(typename T::vec8, qa[ks]),
                           __builtin_bit_cast(typename T::vec8, kb[tt][ks]), acc);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) part[tt] += wv[i] * fmaxf(acc[i], 0.f);
+        for (int i = 0; i < 16; ++i) part[tt] += wv[i] * (RELU ? fmaxf(acc[i], 0.f) : acc[i]);
       }
     }
 #pragma unroll
@@ -221,10 +229,12 @@ __device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
 
 // k-th largest key among included keys, all of which lie in [kmin, kmax].
 // The radix passes work on key - kmin and start at the top bit of the range,
-// so the first 11-bit histogram already spreads over all 2048 bins (scores
+// so the first 13-bit histogram already spreads over all 8192 bins (scores
 // share sign and exponent bits; a histogram of the raw top bits would pile
-// them into a few bins).  load(i, key[4], inc[4]) supplies group i < ngroups.
-// Requires (#included) >= k >= 1.
+// them into a few bins); a range of up to 26 bits takes two passes.
+// visit(fn) calls fn(key) for every included key of the calling thread.
+// Requires (#included) >= k >= 1.  `hist` must be zero on entry and is zero
+// again on return (each owner clears its bins after reading them).
 template <typename Visit>
 __device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Visit visit, uint32_t* hist,
                                         int* scratch, int* bcast) {
@@ -234,11 +244,9 @@ __device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Vis
   uint32_t prefix = 0, pmask = 0;
   int remaining = k, cnt_eq = 0;
 #pragma unroll 1
-  for (int hi = L; hi > 0; hi -= 11) {
-    const int lo = hi > 11 ? hi - 11 : 0;
+  for (int hi = L; hi > 0; hi -= kDigitBits) {
+    const int lo = hi > kDigitBits ? hi - kDigitBits : 0;
     const uint32_t dmask = (1u << (hi - lo)) - 1u;
-    for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0;
-    __syncthreads();
     visit([&](uint32_t key) {
       const uint32_t d = key - kmin;
       if ((d & pmask) == prefix) atomicAdd(&hist[(d >> lo) & dmask], 1u);
@@ -252,18 +260,21 @@ __device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Vis
 #pragma unroll
     for (int j = 0; j < kBinsPerThread; ++j) {
       cnt[j] = static_cast<int>(hist[tb * kBinsPerThread + j]);
+      hist[tb * kBinsPerThread + j] = 0u;  // ready for the next pass / call
       sum += cnt[j];
     }
     int total;
     int acc = block_exclusive_scan(sum, scratch, &total);
+    if (acc < remaining && remaining <= acc + sum) {
 #pragma unroll
-    for (int j = kBinsPerThread - 1; j >= 0; --j) {
-      if (acc < remaining && remaining <= acc + cnt[j]) {
-        bcast[0] = tb * kBinsPerThread + j;
-        bcast[1] = acc;
-        bcast[2] = cnt[j];
+      for (int j = kBinsPerThread - 1; j >= 0; --j) {
+        if (acc < remaining && remaining <= acc + cnt[j]) {
+          bcast[0] = tb * kBinsPerThread + j;
+          bcast[1] = acc;
+          bcast[2] = cnt[j];
+        }
+        acc += cnt[j];
       }
-      acc += cnt[j];
     }
     __syncthreads();
     prefix |= static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bcast[0])) << lo;
@@ -336,6 +347,50 @@ __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, 
 
 __device__ inline int lane16(uint64_t v, int q) { return static_cast<int>((v >> (16 * q)) & 0xffffu); }
 
+// Exclusive block scan of eight packed 16-bit counters (two 64-bit words;
+// every counter's block total must stay below 65536).  One pass for all
+// eight: the wave scans shuffle 32-bit halves, the 8 wave totals go through
+// LDS.  Totals are wave-uniform.
+__device__ inline void block_exclusive_scan8(uint64_t (&v)[2], uint64_t* scratch, uint64_t (&total)[2]) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  uint64_t x[2] = {v[0], v[1]};
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t lo = __shfl_up(static_cast<uint32_t>(x[h]), d, 64);
+      const uint32_t hi = __shfl_up(static_cast<uint32_t>(x[h] >> 32), d, 64);
+      if (lane >= d) x[h] += (static_cast<uint64_t>(hi) << 32) | lo;
+    }
+  }
+  if (lane == 63) {
+    scratch[2 * wid] = x[0];
+    scratch[2 * wid + 1] = x[1];
+  }
+  __syncthreads();
+  uint64_t before[2] = {0, 0}, tot[2] = {0, 0};
+  for (int w = 0; w < nw; ++w) {  // every thread reads the nw wave totals
+    const uint64_t t0 = scratch[2 * w], t1 = scratch[2 * w + 1];
+    if (w < wid) {
+      before[0] += t0;
+      before[1] += t1;
+    }
+    tot[0] += t0;
+    tot[1] += t1;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v[h] = before[h] + x[h] - v[h];
+    total[h] = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tot[h] >> 32))) << 32) |
+               static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tot[h])));
+  }
+  __syncthreads();  // scratch is reused by the next scan
+}
+
+__device__ inline int lane16x8(const uint64_t (&v)[2], int i) { return lane16(v[i >> 2], i & 3); }
+
 // Score keys of tokens [t, t + 4) of one score row (tokens >= n excluded).
 __device__ inline void load_score_keys(const float* s, int n, int t, uint32_t* key, bool* inc) {
   if (t + 3 < n) {
@@ -404,10 +459,10 @@ __device__ __forceinline__ int select_victims(int c, int m, const uint32_t* stab
     }
   }
   const int nonhit = block_sum(local, scratch);
-  block_minmax(lo, hi, red);
   const bool take_all = m >= nonhit;
   SelectOut sel{0, 0, 0};
   if (!take_all) {
+    block_minmax(lo, hi, red);
     sel = radix_select(
         static_cast<int>(ceil_div(c, 4)), m, lo, hi,
         [&](int g, uint32_t* key, bool* inc) {
@@ -583,11 +638,14 @@ __device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int 
 // the workspace on every pass (any source length).
 template <int RES>
 __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, LimWs w) {
+  static_assert(RES <= 8, "the packed classification scan holds eight chunks");
   __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint64_t scratch64[2 * (kManageThreads / 64)];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kTopK];
+  __shared__ int lds_miss[kTopK];
   __shared__ uint32_t lds_stab[kLdsSlots];
   __shared__ uint32_t lds_skey[kLdsSlots];
   const int b = blockIdx.x;
@@ -606,41 +664,51 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   const bool lds_tables = c <= kLdsSlots;
   uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kSlotStride;
   uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kSlotStride;
-  int32_t* misses = w.miss_list + static_cast<int64_t>(b) * kUnionCap;
+  int32_t* misses = lds_miss;
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   int eq_run = 0, miss_run = 0;
   if constexpr (RES > 0) {
     // Scores and pool slots of all the request's tokens, loaded once.  A
     // slot is kept as 16 bits: 0 <= slot < C (C <= 16383) or 0xffff for
-    // "not cached", which is all the ordered pass distinguishes.
+    // "not cached", which is all the ordered pass distinguishes.  Entries at
+    // t >= n hold whatever the buffers hold there; every later use tests
+    // t < n (masking at load time would let the compiler turn the vector
+    // loads into guarded scalar loads, one wait each).
     uint32_t u[RES][kItems];
     uint32_t pk[RES][kItems / 2];
     auto p16 = [c](int32_t v) -> uint32_t { return (v >= 0 && v < c) ? static_cast<uint32_t>(v) : 0xffffu; };
+    // The row buffers hold cap entries (cap a multiple of 128): a thread's
+    // 8-token group either lies inside or starts at t0 >= cap, whose load is
+    // redirected to the last group and ignored (t0 >= cap >= n).  So every
+    // load is unconditional, and all 32 of a thread's loads are in flight
+    // together.
+    uint4 raw_s[RES][2];
+    int4 raw_p[RES][2];
 #pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {
+    for (int ch = 0; ch < RES; ++ch) {  // all loads first ...
       const int t0 = ch * kChunk + tid * kItems;
-      if (t0 + kItems <= n) {
-        const float4 x = *reinterpret_cast<const float4*>(s + t0);
-        const float4 y = *reinterpret_cast<const float4*>(s + t0 + 4);
-        const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
-        const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
-        u[ch][0] = score_key(x.x); u[ch][1] = score_key(x.y); u[ch][2] = score_key(x.z); u[ch][3] = score_key(x.w);
-        u[ch][4] = score_key(y.x); u[ch][5] = score_key(y.y); u[ch][6] = score_key(y.z); u[ch][7] = score_key(y.w);
-        pk[ch][0] = p16(pa.x) | (p16(pa.y) << 16);
-        pk[ch][1] = p16(pa.z) | (p16(pa.w) << 16);
-        pk[ch][2] = p16(pb.x) | (p16(pb.y) << 16);
-        pk[ch][3] = p16(pb.z) | (p16(pb.w) << 16);
-      } else {
+      const int64_t tl = t0 < cap ? t0 : cap - kItems;
+      raw_s[ch][0] = *reinterpret_cast<const uint4*>(s + tl);
+      raw_s[ch][1] = *reinterpret_cast<const uint4*>(s + tl + 4);
+      raw_p[ch][0] = *reinterpret_cast<const int4*>(pool + tl);
+      raw_p[ch][1] = *reinterpret_cast<const int4*>(pool + tl + 4);
+    }
 #pragma unroll
-        for (int e = 0; e < kItems; ++e) u[ch][e] = t0 + e < n ? score_key(s[t0 + e]) : 0u;
+    for (int ch = 0; ch < RES; ++ch) {  // ... then the conversions
+      const uint32_t xs[kItems] = {raw_s[ch][0].x, raw_s[ch][0].y, raw_s[ch][0].z, raw_s[ch][0].w,
+                                   raw_s[ch][1].x, raw_s[ch][1].y, raw_s[ch][1].z, raw_s[ch][1].w};
+      const int32_t ps[kItems] = {raw_p[ch][0].x, raw_p[ch][0].y, raw_p[ch][0].z, raw_p[ch][0].w,
+                                  raw_p[ch][1].x, raw_p[ch][1].y, raw_p[ch][1].z, raw_p[ch][1].w};
+      uint32_t pv[kItems];
 #pragma unroll
-        for (int e = 0; e < kItems / 2; ++e) {
-          const uint32_t v0 = t0 + 2 * e < n ? p16(pool[t0 + 2 * e]) : 0xffffu;
-          const uint32_t v1 = t0 + 2 * e + 1 < n ? p16(pool[t0 + 2 * e + 1]) : 0xffffu;
-          pk[ch][e] = v0 | (v1 << 16);
-        }
+      for (int e = 0; e < kItems; ++e) {
+        u[ch][e] = score_key(__uint_as_float(xs[e]));
+        pv[e] = p16(ps[e]);
       }
+#pragma unroll
+      for (int e = 0; e < kItems / 2; ++e) pk[ch][e] = pv[2 * e] | (pv[2 * e + 1] << 16);
     }
     uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
@@ -662,22 +730,66 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
               if (ch * kChunk + tid * kItems + e < n) fn(u[ch][e]);
         },
         hist, scratch, bcast);
+    // One ordered classification pass: token order is (chunk, thread, item),
+    // so the eight chunks' miss counts go through one packed block scan.
     const bool need_rank = sel.cnt_eq != sel.need_eq;
+    uint32_t selm[RES], eqm[RES], cachm[RES];
 #pragma unroll
     for (int ch = 0; ch < RES; ++ch) {
-      const int base = ch * kChunk;
-      if (base >= n) break;  // uniform
-      int32_t slot[kItems];
+      selm[ch] = eqm[ch] = cachm[ch] = 0u;
 #pragma unroll
       for (int e = 0; e < kItems; ++e) {
-        const uint32_t v = (pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        slot[e] = v == 0xffffu ? -1 : static_cast<int32_t>(v);
+        if (ch * kChunk + tid * kItems + e >= n) continue;
+        if (u[ch][e] > sel.thresh) selm[ch] |= 1u << e;
+        if (u[ch][e] == sel.thresh) eqm[ch] |= 1u << e;
+        if (((pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu) != 0xffffu) cachm[ch] |= 1u << e;
       }
-      const int t0 = base + tid * kItems;
-      bool in[kItems];
+    }
+    if (need_rank) {  // ties at the threshold: the lowest tokens first
+      uint64_t cnt[2] = {0, 0}, tot[2];
 #pragma unroll
-      for (int e = 0; e < kItems; ++e) in[e] = t0 + e < n;
-      mtp0_classify8(t0, u[ch], slot, in, c, sel, need_rank, eq_run, miss_run, misses, stab, skey, scratch);
+      for (int ch = 0; ch < RES; ++ch) cnt[ch >> 2] |= static_cast<uint64_t>(__popc(eqm[ch])) << (16 * (ch & 3));
+      block_exclusive_scan8(cnt, scratch64, tot);
+      int before = 0;
+#pragma unroll
+      for (int ch = 0; ch < RES; ++ch) {
+        int rk = before + lane16x8(cnt, ch);
+#pragma unroll
+        for (int e = 0; e < kItems; ++e)
+          if ((eqm[ch] >> e) & 1u) {
+            if (rk < sel.need_eq) selm[ch] |= 1u << e;
+            ++rk;
+          }
+        before += lane16x8(tot, ch);
+      }
+    } else {
+#pragma unroll
+      for (int ch = 0; ch < RES; ++ch) selm[ch] |= eqm[ch];
+    }
+    uint64_t cnt[2] = {0, 0}, tot[2];
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch)
+      cnt[ch >> 2] |= static_cast<uint64_t>(__popc(selm[ch] & ~cachm[ch])) << (16 * (ch & 3));
+    block_exclusive_scan8(cnt, scratch64, tot);
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch) {
+      int pos = miss_run + lane16x8(cnt, ch);
+      const int t0 = ch * kChunk + tid * kItems;
+      const uint32_t missm = selm[ch] & ~cachm[ch];
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) {
+        if ((missm >> e) & 1u) misses[pos++] = t0 + e;
+        if ((cachm[ch] >> e) & 1u) {
+          const uint32_t slot = (pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+          if ((selm[ch] >> e) & 1u) {
+            stab[slot] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
+          } else {
+            stab[slot] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
+            skey[slot] = u[ch][e];
+          }
+        }
+      }
+      miss_run += lane16x8(tot, ch);
     }
   } else {
     const int ngroups = static_cast<int>(ceil_div(n, 4));
@@ -746,6 +858,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   const int ngroups = static_cast<int>(ceil_div(n, 4));
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   for (int q = 0; q < kMtpQueries; ++q) {
     const float* sq = s + q * cap;
     uint32_t lo = 0xffffffffu, hi = 0u;
@@ -960,17 +1073,173 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   if (tid == 0) a.miss_counts[b] = m;
 }
 
+// ---------------------------------------------------------------------------
+// 3. First-decode LIDU initialisation (nanovllm/models/dsa_offload_ops.py:251-411).
+
+struct InitWs {
+  float* scores;  // [S_cap]
+  int32_t* src;   // [16384] selected tokens, ascending
+  int32_t* dst;   // [16384] their slots
+  int32_t* count; // list length
+};
+
+InitWs carve_init(void* base, int64_t cap) {
+  char* p = static_cast<char*>(base);
+  InitWs w;
+  w.scores = reinterpret_cast<float*>(p);
+  p += align256(sizeof(float) * cap);
+  w.src = reinterpret_cast<int32_t*>(p);
+  p += align256(sizeof(int32_t) * kSlotStride);
+  w.dst = reinterpret_cast<int32_t*>(p);
+  p += align256(sizeof(int32_t) * kSlotStride);
+  w.count = reinterpret_cast<int32_t*>(p);
+  return w;
+}
+
+// One workgroup: the C largest linear scores of tokens [0, n) (ties at the
+// threshold to the lower tokens), slot i to the i-th smallest selected token,
+// the pool row rewritten over its whole length (-1 outside the selection),
+// and the (token, slot) copy list.
+__global__ __launch_bounds__(kManageThreads) void lidu_init_kernel(const float* s, int n, int c, int32_t* pool_row,
+                                                                   int64_t row_len, InitWs w) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  const int ngroups = static_cast<int>(ceil_div(n, 4));
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int g = tid; g < ngroups; g += kManageThreads) {
+    uint32_t key[4];
+    bool inc[4];
+    load_score_keys(s, n, 4 * g, key, inc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (inc[e]) {
+        lo = min(lo, key[e]);
+        hi = max(hi, key[e]);
+      }
+  }
+  block_minmax(lo, hi, red);
+  const SelectOut sel = radix_select(
+      ngroups, c, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); }, hist,
+      scratch, bcast);
+  const bool need_rank = sel.cnt_eq != sel.need_eq;
+  int eq_run = 0, run = 0;
+  for (int64_t base = 0; base < row_len; base += kChunk) {
+    const int64_t t0 = base + static_cast<int64_t>(tid) * kItems;
+    unsigned selmask = 0, eqmask = 0;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      const int64_t t = t0 + e;
+      if (t >= n) continue;
+      const uint32_t u = score_key(s[t]);
+      if (u > sel.thresh) selmask |= 1u << e;
+      if (u == sel.thresh) eqmask |= 1u << e;
+    }
+    if (need_rank) {
+      int tot;
+      int rk = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if ((eqmask >> e) & 1u) {
+          if (rk < sel.need_eq) selmask |= 1u << e;
+          ++rk;
+        }
+      eq_run += tot;
+    } else {
+      selmask |= eqmask;
+    }
+    int tot;
+    int pos = run + block_exclusive_scan(__popc(selmask), scratch, &tot);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      const int64_t t = t0 + e;
+      if (t >= row_len) continue;
+      if ((selmask >> e) & 1u) {
+        pool_row[t] = pos;
+        if (pos < kSlotStride) {
+          w.src[pos] = static_cast<int32_t>(t);
+          w.dst[pos] = pos;
+        }
+        ++pos;
+      } else {
+        pool_row[t] = -1;
+      }
+    }
+    run += tot;
+  }
+  if (tid == 0) *w.count = run;
+}
+
+// One workgroup: the (token, slot) list of every entry >= 0 of an owner's
+// pool row, ascending token (dsa_offload_ops.py:385-388); the count may
+// exceed the list capacity (the caller checks it).
+__global__ __launch_bounds__(kManageThreads) void lidu_shared_kernel(const int32_t* pool_row, int64_t row_len,
+                                                                     InitWs w) {
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  int run = 0;
+  for (int64_t base = 0; base < row_len; base += kChunk) {
+    const int64_t t0 = base + static_cast<int64_t>(tid) * kItems;
+    int32_t v[kItems];
+    unsigned mask = 0;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      v[e] = t0 + e < row_len ? pool_row[t0 + e] : -1;
+      if (v[e] >= 0) mask |= 1u << e;
+    }
+    int tot;
+    int pos = run + block_exclusive_scan(__popc(mask), scratch, &tot);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e)
+      if ((mask >> e) & 1u) {
+        if (pos < kSlotStride) {
+          w.src[pos] = static_cast<int32_t>(t0 + e);
+          w.dst[pos] = v[e];
+        }
+        ++pos;
+      }
+    run += tot;
+  }
+  if (tid == 0) *w.count = run;
+}
+
+template <typename T>
+hipError_t launch_lidu_scores(const LiduInitArgs& a, const InitWs& w, hipStream_t stream) {
+  LimArgs la{};
+  la.query = a.query;
+  la.weights = a.weights;
+  la.key_cache = a.key_cache;
+  la.block_table = a.index_table;
+  la.cols = a.index_cols;
+  la.key_blocks = a.key_blocks;
+  la.source_capacity = a.row_len;
+  la.heads = a.heads;
+  la.batch = 1;
+  const dim3 grid(static_cast<uint32_t>(ceil_div(ceil_div(a.n, kBlock), kScoreWaves)), 1);
+  if (a.heads == 32) {
+    launch_kernel(kKernLimScore, lim_score_kernel<T, 32, 1, false>, grid, dim3(kScoreWaves * kWave), stream, la,
+                  w.scores, 0, static_cast<int>(a.n));
+  } else {
+    launch_kernel(kKernLimScore, lim_score_kernel<T, 64, 1, false>, grid, dim3(kScoreWaves * kWave), stream, la,
+                  w.scores, 0, static_cast<int>(a.n));
+  }
+  return hipGetLastError();
+}
+
 template <typename T, int Q>
 hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   const LimWs w = carve(a.workspace, a.batch, a.source_capacity, Q);
   const dim3 grid(static_cast<uint32_t>(ceil_div(a.cols, kScoreWaves)), static_cast<uint32_t>(a.batch));
   const int mtp = Q > 1 ? 1 : 0;
   if (a.heads == 32) {
-    launch_kernel(kKernLimScore, lim_score_kernel<T, 32, Q>, grid, dim3(kScoreWaves * kWave), stream, a, w.scores,
-                  mtp);
+    launch_kernel(kKernLimScore, lim_score_kernel<T, 32, Q, true>, grid, dim3(kScoreWaves * kWave), stream, a,
+                  w.scores, mtp, -1);
   } else {
-    launch_kernel(kKernLimScore, lim_score_kernel<T, 64, Q>, grid, dim3(kScoreWaves * kWave), stream, a, w.scores,
-                  mtp);
+    launch_kernel(kKernLimScore, lim_score_kernel<T, 64, Q, true>, grid, dim3(kScoreWaves * kWave), stream, a,
+                  w.scores, mtp, -1);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -993,6 +1262,52 @@ size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries) 
   total += align256(sizeof(int32_t) * batch * kUnionCap);
   if (queries > 1) total += align256(static_cast<size_t>(batch) * source_capacity);
   return total;
+}
+
+size_t lidu_init_workspace_bytes(int64_t source_capacity) {
+  return align256(sizeof(float) * source_capacity) + 2 * align256(sizeof(int32_t) * kSlotStride) + 256;
+}
+
+int64_t lidu_list_capacity() { return kSlotStride; }
+
+hipError_t launch_lidu_init(const LiduInitArgs& a, hipStream_t stream) {
+  const InitWs w = carve_init(a.workspace, a.row_len);
+  hipError_t e = a.elem == Elem::kBf16 ? launch_lidu_scores<Bf16>(a, w, stream) : launch_lidu_scores<F16>(a, w, stream);
+  if (e != hipSuccess) return e;
+  launch_kernel(kKernLiduInit, lidu_init_kernel, dim3(1), dim3(kManageThreads), stream,
+                static_cast<const float*>(w.scores), static_cast<int>(a.n), static_cast<int>(a.c), a.pool_row,
+                a.row_len, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_lidu_shared_list(const LiduInitArgs& a, hipStream_t stream) {
+  const InitWs w = carve_init(a.workspace, a.row_len);
+  launch_kernel(kKernLiduShared, lidu_shared_kernel, dim3(1), dim3(kManageThreads), stream,
+                static_cast<const int32_t*>(a.pool_row), a.row_len, w);
+  return hipGetLastError();
+}
+
+const int32_t* lidu_list_count(const LiduInitArgs& a) { return carve_init(a.workspace, a.row_len).count; }
+
+hipError_t launch_lidu_copy(const LiduInitArgs& a, hipStream_t stream) {
+  const InitWs w = carve_init(a.workspace, a.row_len);
+  ScatterArgs sa{};
+  sa.src_ids = w.src;
+  sa.dst_slots = w.dst;
+  sa.copy_counts = w.count;
+  sa.hbm_table = a.hbm_table;
+  sa.dram_table = a.dram_table;
+  sa.hbm_kpe = a.hbm_kpe;
+  sa.hbm_ckv = a.hbm_ckv;
+  sa.dram_kpe = a.dram_kpe;
+  sa.dram_ckv = a.dram_ckv;
+  sa.batch = 1;
+  sa.cap = a.c;
+  sa.hbm_cols = a.hbm_cols;
+  sa.dram_cols = a.dram_cols;
+  sa.hbm_blocks = a.hbm_blocks;
+  sa.dram_blocks = a.dram_blocks;
+  return launch_scatter_copy(sa, stream);
 }
 
 hipError_t launch_fused_li_manage(const LimArgs& a, hipStream_t stream) {

@@ -170,7 +170,7 @@ int nvdsa_profile_end(float* durations_ms, int32_t* kernel_ids, int32_t capacity
 const char* nvdsa_kernel_name(int32_t kernel_id) {
   static const char* names[] = {"scatter_copy_kernel", "lim_score_kernel",   "lim_manage_kernel",
                                 "lim_manage_mtp_kernel", "sfa_split_kernel", "sfa_split_kernel_fused",
-                                "sfa_combine_kernel"};
+                                "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel"};
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }
@@ -427,6 +427,180 @@ int nvdsa_scatter_copy(const nvdsa_tensor* src_ids, const nvdsa_tensor* dst_slot
   a.hbm_blocks = std::min(sz(hbm_k_rope, 0), sz(hbm_kv_cache, 0));
   a.dram_blocks = std::min(sz(dram_k_rope, 0), sz(dram_kv_cache, 0));
   return launch_status(nvdsa::launch_scatter_copy(a, static_cast<hipStream_t>(stream)), "scatter_copy");
+}
+
+// ------------------------------------------------------------------------
+// First-decode LIDU initialisation (nanovllm/models/dsa_offload_ops.py:251-411).
+namespace {
+
+// Cache and table checks shared by the two initialisation entry points (the
+// 3-D cache views scatter_copy takes, 1-D table rows of one request).
+void check_lidu_copy(Check& c, const nvdsa_tensor* slots_row, const nvdsa_tensor* hbm_kpe,
+                     const nvdsa_tensor* hbm_ckv, const nvdsa_tensor* dram_kpe, const nvdsa_tensor* dram_ckv,
+                     const nvdsa_tensor* hbm_table, const nvdsa_tensor* dram_table) {
+  c.need(dims_are(slots_row, 1) && slots_row->dtype == NVDSA_INT32, NVDSA_ERR_SHAPE,
+         "cache_slots_row must be a 1-D int32 pool row")
+      .need(dims_are(hbm_kpe, 3) && sz(hbm_kpe, 1) == 128 && sz(hbm_kpe, 2) == 64, NVDSA_ERR_SHAPE,
+            "HBM KPE must be [blocks, 128, 64]")
+      .need(dims_are(hbm_ckv, 3) && sz(hbm_ckv, 1) == 128 && sz(hbm_ckv, 2) == 512, NVDSA_ERR_SHAPE,
+            "HBM CKV must be [blocks, 128, 512]")
+      .need(dims_are(dram_kpe, 3) && sz(dram_kpe, 1) == 128 && sz(dram_kpe, 2) == 64, NVDSA_ERR_SHAPE,
+            "DRAM KPE must be [blocks, 128, 64]")
+      .need(dims_are(dram_ckv, 3) && sz(dram_ckv, 1) == 128 && sz(dram_ckv, 2) == 512, NVDSA_ERR_SHAPE,
+            "DRAM CKV must be [blocks, 128, 512]")
+      .need(dims_are(hbm_table, 1) && dims_are(dram_table, 1) && hbm_table->dtype == NVDSA_INT32 &&
+                dram_table->dtype == NVDSA_INT32,
+            NVDSA_ERR_SHAPE, "block tables must be 1-D int32 rows")
+      .need(is_half(hbm_kpe) && hbm_ckv->dtype == hbm_kpe->dtype && dram_kpe->dtype == hbm_kpe->dtype &&
+                dram_ckv->dtype == hbm_kpe->dtype,
+            NVDSA_ERR_DTYPE, "all CKV/KPE tensors must share one 16-bit dtype");
+}
+
+void fill_lidu_copy(nvdsa::LiduInitArgs& a, const nvdsa_tensor* slots_row, const nvdsa_tensor* hbm_kpe,
+                    const nvdsa_tensor* hbm_ckv, const nvdsa_tensor* dram_kpe, const nvdsa_tensor* dram_ckv,
+                    const nvdsa_tensor* hbm_table, const nvdsa_tensor* dram_table, int64_t c, void* workspace,
+                    size_t workspace_bytes) {
+  a.c = c;
+  a.pool_row = static_cast<int32_t*>(slots_row->data);
+  a.row_len = sz(slots_row, 0);
+  a.hbm_kpe = hbm_kpe->data;
+  a.hbm_ckv = hbm_ckv->data;
+  a.dram_kpe = dram_kpe->data;
+  a.dram_ckv = dram_ckv->data;
+  a.hbm_table = static_cast<const int32_t*>(hbm_table->data);
+  a.hbm_cols = sz(hbm_table, 0);
+  a.hbm_blocks = std::min(sz(hbm_kpe, 0), sz(hbm_ckv, 0));
+  a.dram_table = static_cast<const int32_t*>(dram_table->data);
+  a.dram_cols = sz(dram_table, 0);
+  a.dram_blocks = std::min(sz(dram_kpe, 0), sz(dram_ckv, 0));
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+}
+
+}  // namespace
+
+size_t nvdsa_initialize_lidu_row_workspace_size(int64_t source_capacity) {
+  if (source_capacity < 0) return 0;
+  return nvdsa::lidu_init_workspace_bytes(source_capacity);
+}
+
+int nvdsa_initialize_lidu_row(const nvdsa_tensor* query, const nvdsa_tensor* weights,
+                              const nvdsa_tensor* index_cache, const nvdsa_tensor* index_block_table,
+                              int64_t candidate_len, int64_t cache_tokens, const nvdsa_tensor* cache_slots_row,
+                              const nvdsa_tensor* hbm_kpe, const nvdsa_tensor* hbm_ckv, const nvdsa_tensor* dram_kpe,
+                              const nvdsa_tensor* dram_ckv, const nvdsa_tensor* hbm_block_table,
+                              const nvdsa_tensor* dram_block_table, int64_t block_size, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const nvdsa_tensor* const all[] = {query,   weights, index_cache, index_block_table, cache_slots_row,
+                                     hbm_kpe, hbm_ckv, dram_kpe,    dram_ckv,          hbm_block_table,
+                                     dram_block_table};
+  if (!all_nonnull(all)) return fail(NVDSA_ERR_ARG, "initialize_lidu_row: null tensor argument");
+  if (cache_tokens <= 0) {  // no cache budget: nothing to initialise
+    g_last_error.clear();
+    return NVDSA_OK;
+  }
+  char msg[160];
+  // The reference's argument errors (dsa_offload_ops.py:280-294), then this
+  // implementation's limits.
+  if (cache_tokens < nvdsa::kTopK) {
+    std::snprintf(msg, sizeof(msg), "LIDU nonzero cache budget must be >= %d, got %lld.", nvdsa::kTopK,
+                  static_cast<long long>(cache_tokens));
+    return fail(NVDSA_ERR_ARG, msg);
+  }
+  if (candidate_len < cache_tokens) {
+    std::snprintf(msg, sizeof(msg), "LIDU cache budget %lld exceeds source length %lld.",
+                  static_cast<long long>(cache_tokens), static_cast<long long>(candidate_len));
+    return fail(NVDSA_ERR_ARG, msg);
+  }
+  if (block_size <= 0 || candidate_len % block_size) return fail(NVDSA_ERR_ARG, "LIDU source must consist only of complete blocks.");
+  Check c("initialize_lidu_row");
+  c.need(block_size == nvdsa::kBlock, NVDSA_ERR_ARG, "block_size must be 128")
+      .need(cache_tokens <= nvdsa::kMaxCacheTokens, NVDSA_ERR_ARG, "cache budget must be <= 16383 slots")
+      .need(candidate_len <= nvdsa::kMaxActualSeqLen, NVDSA_ERR_ARG, "candidate_len must be < 2^21")
+      .need((dims_are(query, 2) || (dims_are(query, 3) && sz(query, 0) == 1)) && sz(query, query->ndim - 1) == 128,
+            NVDSA_ERR_SHAPE, "query must be [N, 128]")
+      .need(sz(query, query->ndim - 2) == 32 || sz(query, query->ndim - 2) == 64, NVDSA_ERR_SHAPE,
+            "index head count must be 32 or 64")
+      .need(numel(weights) == sz(query, query->ndim - 2), NVDSA_ERR_SHAPE, "weights must hold one value per head")
+      .need(dims_are(index_cache, 4) && sz(index_cache, 1) == 128 && sz(index_cache, 2) == 1 &&
+                sz(index_cache, 3) == 128,
+            NVDSA_ERR_SHAPE, "index cache must be [blocks, 128, 1, 128]")
+      .need(dims_are(index_block_table, 1) && index_block_table->dtype == NVDSA_INT32, NVDSA_ERR_SHAPE,
+            "index_block_table must be a 1-D int32 row")
+      .need(candidate_len <= sz(index_block_table, 0) * 128, NVDSA_ERR_SHAPE,
+            "candidate_len exceeds the index block table")
+      .need(is_half(query) && weights->dtype == query->dtype && index_cache->dtype == query->dtype, NVDSA_ERR_DTYPE,
+            "query, weights and index cache must share one 16-bit dtype");
+  if (c.ok()) check_lidu_copy(c, cache_slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table);
+  if (c.ok()) {
+    c.need(candidate_len <= sz(cache_slots_row, 0), NVDSA_ERR_SHAPE, "cache_slots_row is shorter than the source");
+    check_common(c, all, query->device, dram_kpe, dram_ckv);
+    c.need(aligned16(query) && aligned16(index_cache) && aligned16(hbm_kpe) && aligned16(hbm_ckv) &&
+               aligned16(dram_kpe) && aligned16(dram_ckv),
+           NVDSA_ERR_LAYOUT, "query, index cache and KV caches must be 16-byte aligned");
+    c.need(workspace != nullptr && workspace_bytes >= nvdsa::lidu_init_workspace_bytes(sz(cache_slots_row, 0)),
+           NVDSA_ERR_WORKSPACE, "workspace too small");
+  }
+  if (!c.ok()) return c.finish();
+  nvdsa::LiduInitArgs a{};
+  a.query = query->data;
+  a.weights = weights->data;
+  a.key_cache = index_cache->data;
+  a.index_table = static_cast<const int32_t*>(index_block_table->data);
+  a.index_cols = sz(index_block_table, 0);
+  a.key_blocks = sz(index_cache, 0);
+  a.heads = sz(query, query->ndim - 2);
+  a.elem = elem_of(query);
+  a.n = candidate_len;
+  fill_lidu_copy(a, cache_slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table,
+                 cache_tokens, workspace, workspace_bytes);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = nvdsa::launch_lidu_init(a, st);
+  if (e == hipSuccess) e = nvdsa::launch_lidu_copy(a, st);
+  return launch_status(e, "initialize_lidu_row");
+}
+
+int nvdsa_initialize_lidu_row_shared(const nvdsa_tensor* cache_slots_row, int64_t cache_tokens,
+                                     const nvdsa_tensor* hbm_kpe, const nvdsa_tensor* hbm_ckv,
+                                     const nvdsa_tensor* dram_kpe, const nvdsa_tensor* dram_ckv,
+                                     const nvdsa_tensor* hbm_block_table, const nvdsa_tensor* dram_block_table,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  const nvdsa_tensor* const all[] = {cache_slots_row, hbm_kpe,         hbm_ckv,         dram_kpe,
+                                     dram_ckv,        hbm_block_table, dram_block_table};
+  if (!all_nonnull(all)) return fail(NVDSA_ERR_ARG, "initialize_lidu_row_shared: null tensor argument");
+  if (cache_tokens <= 0) {
+    g_last_error.clear();
+    return NVDSA_OK;
+  }
+  Check c("initialize_lidu_row_shared");
+  c.need(cache_tokens <= nvdsa::kMaxCacheTokens, NVDSA_ERR_ARG, "cache budget must be <= 16383 slots");
+  check_lidu_copy(c, cache_slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table);
+  if (c.ok()) {
+    check_common(c, all, hbm_kpe->device, dram_kpe, dram_ckv);
+    c.need(aligned16(hbm_kpe) && aligned16(hbm_ckv) && aligned16(dram_kpe) && aligned16(dram_ckv), NVDSA_ERR_LAYOUT,
+           "KV caches must be 16-byte aligned")
+        .need(workspace != nullptr && workspace_bytes >= nvdsa::lidu_init_workspace_bytes(sz(cache_slots_row, 0)),
+              NVDSA_ERR_WORKSPACE, "workspace too small");
+  }
+  if (!c.ok()) return c.finish();
+  nvdsa::LiduInitArgs a{};
+  fill_lidu_copy(a, cache_slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table,
+                 cache_tokens, workspace, workspace_bytes);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = nvdsa::launch_lidu_shared_list(a, st);
+  // The reference checks the cached count before copying (its nonzero()
+  // synchronises too): read the count the list kernel wrote.
+  int32_t found = -1;
+  if (e == hipSuccess) e = hipMemcpyAsync(&found, nvdsa::lidu_list_count(a), sizeof(found), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return launch_status(e, "initialize_lidu_row_shared");
+  if (found != cache_tokens) {
+    char msg[160];
+    std::snprintf(msg, sizeof(msg), "Shared layer LIDU initialization found %d cached tokens, expected %lld.", found,
+                  static_cast<long long>(cache_tokens));
+    return fail(NVDSA_ERR_RUNTIME, msg);
+  }
+  return launch_status(nvdsa::launch_lidu_copy(a, st), "initialize_lidu_row_shared");
 }
 
 // ------------------------------------------------------------------------

@@ -20,7 +20,9 @@ enum KernelId : int {
   kKernSfaSplit = 4,
   kKernSfaSplitFused = 5,
   kKernSfaCombine = 6,
-  kKernCount = 7
+  kKernLiduInit = 7,
+  kKernLiduShared = 8,
+  kKernCount = 9
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.
@@ -91,6 +93,44 @@ struct LimArgs {
 size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries);
 hipError_t launch_fused_li_manage(const LimArgs& a, hipStream_t stream);
 hipError_t launch_fused_li_manage_mtp(const LimArgs& a, hipStream_t stream);
+
+// ---- first-decode LIDU initialisation -------------------------------------
+struct LiduInitArgs {
+  const void* query;            // [H, 128] (one request)
+  const void* weights;          // [H]
+  const void* key_cache;        // [key_blocks, 128, 1, 128]
+  const int32_t* index_table;   // [index_cols]
+  int64_t index_cols;
+  int64_t key_blocks;
+  int64_t heads;
+  Elem elem;
+  int64_t n;                    // candidate tokens (whole blocks)
+  int64_t c;                    // cache budget C
+  int32_t* pool_row;            // [row_len] token -> slot
+  int64_t row_len;
+  void* hbm_kpe;                // [hbm_blocks, 128, 64]
+  void* hbm_ckv;                // [hbm_blocks, 128, 512]
+  const void* dram_kpe;
+  const void* dram_ckv;
+  const int32_t* hbm_table;     // [hbm_cols]
+  int64_t hbm_cols;
+  int64_t hbm_blocks;
+  const int32_t* dram_table;    // [dram_cols]
+  int64_t dram_cols;
+  int64_t dram_blocks;
+  void* workspace;
+  size_t workspace_bytes;
+};
+size_t lidu_init_workspace_bytes(int64_t source_capacity);
+int64_t lidu_list_capacity();
+// Scores, top-C selection, pool row and copy list (then launch_lidu_copy).
+hipError_t launch_lidu_init(const LiduInitArgs& a, hipStream_t stream);
+// Copy list of a shared layer from the owner's pool row; its length is
+// written to lidu_list_count(a) on the device.
+hipError_t launch_lidu_shared_list(const LiduInitArgs& a, hipStream_t stream);
+const int32_t* lidu_list_count(const LiduInitArgs& a);
+// DRAM -> HBM copy of the list (scatter_copy kernel).
+hipError_t launch_lidu_copy(const LiduInitArgs& a, hipStream_t stream);
 
 // ---- sparse-tail attention (+ fused copy) --------------------------------
 struct SfaArgs {

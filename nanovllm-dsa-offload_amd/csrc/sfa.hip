@@ -12,17 +12,22 @@
 //
 // Kernel design (split-KV flash decode):
 //   grid = rows x splits x ceil(heads/64); a 256-thread workgroup owns one
-//   row, one split of its key list and 64 heads (one 16-head MFMA tile per
-//   wavefront).  Keys are processed in tiles of 32; split s takes tiles
-//   s, s+S, s+2S, ... so host-sourced miss rows (a prefix of the list) spread
-//   over all splits.  Each tile is gathered once into LDS in two layouts:
-//   row-major [key][576] for S^T = K . Q^T (v_mfma_f32_16x16x32, A = keys,
-//   B = the wave's queries held in registers) and transposed [512][key] for
-//   O^T = V^T . P^T, whose B operand is the softmax numerator already sitting
-//   in the S^T accumulator lanes.  Online softmax in base 2; a second kernel
-//   merges the per-split (max, sum, numerator) partials.
-//   fused_copy_sfa: tiles holding misses read those rows from host-mapped
-//   DRAM, use them for attention and store them to their HBM slots.
+//   row, one split of its key list and 64 heads (16 heads per wavefront).
+//   Keys are processed in tiles of 32.  The block's 64x576 queries are
+//   staged in LDS once; each tile is gathered row-contiguous into LDS
+//   (conflict-free 16-byte MFMA operand reads).  S^T = K . Q^T and
+//   O^T = V^T . P^T run on v_mfma_f32_16x16x32; the online softmax is in
+//   base 2, and P enters the PV product as a bf16/f16 hi+lo pair so its
+//   rounding stays at fp32 level.  A second kernel merges the per-split
+//   (max, sum, numerator) partials.
+//   fused_copy_sfa (MTP0): a row's miss keys are the first miss_counts
+//   entries of its list.  The first kMissSplitPct percent of a row's splits
+//   take the tiles holding them: each such tile is read once from host-mapped
+//   DRAM, stored to its HBM slots and consumed from LDS.  The other splits
+//   take the HBM-only tiles, so the host-link-bound copy and the HBM-bound
+//   attention run side by side.  fused_copy_sfa_mtp: the union misses are
+//   not tile-aligned to any one query row, so the union is copied first
+//   (scatter_copy) and the MTP attention follows on the same stream.
 #include <cfloat>
 
 #include "nvdsa_common.h"
@@ -43,6 +48,7 @@ constexpr int kMaxSplits = 64;
 constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per window (one key per thread)
 constexpr int kWindowKeys = kWindowTiles * kTileKeys;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMissSplitPct = 20;  // fused: share of a row's splits given the host-sourced tiles
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -427,7 +433,7 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int splits = choose_splits(rows, hgroups);
   SfaArgs args = a;
   // Fused: ~30% of a row's splits handle the host-sourced miss tiles.
-  args.miss_splits = FUSED ? (splits >= 2 ? static_cast<int>((splits * 3 + 9) / 10) : 0) : 0;
+  args.miss_splits = FUSED ? (splits >= 2 ? (splits * kMissSplitPct + 99) / 100 : 0) : 0;
   if (FUSED && args.miss_splits >= splits) args.miss_splits = splits - 1;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
   launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED>,

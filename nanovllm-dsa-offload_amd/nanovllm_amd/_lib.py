@@ -66,6 +66,9 @@ SIGNATURES = {
     "nvdsa_sparse_tail_attention_mtp": ([_P] * 9 + [_DBL, _P, _VP, _SZ, _VP], ctypes.c_int),
     "nvdsa_fused_copy_sfa": ([_P] * 14 + [_DBL, _P, _VP, _SZ, _VP], ctypes.c_int),
     "nvdsa_fused_copy_sfa_mtp": ([_P] * 16 + [_DBL, _P, _VP, _SZ, _VP], ctypes.c_int),
+    "nvdsa_initialize_lidu_row_workspace_size": ([_I64], _SZ),
+    "nvdsa_initialize_lidu_row": ([_P] * 4 + [_I64, _I64] + [_P] * 7 + [_I64, _VP, _SZ, _VP], ctypes.c_int),
+    "nvdsa_initialize_lidu_row_shared": ([_P, _I64] + [_P] * 6 + [_VP, _SZ, _VP], ctypes.c_int),
     "nvdsa_host_mapped_alloc": ([_SZ, ctypes.POINTER(_VP), ctypes.POINTER(_VP)], ctypes.c_int),
     "nvdsa_host_mapped_free": ([_VP], ctypes.c_int),
     "nvdsa_profile_begin": ([ctypes.c_int32], ctypes.c_int),

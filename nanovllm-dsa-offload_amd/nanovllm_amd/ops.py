@@ -125,7 +125,8 @@ class _Workspace:
         return buf.data_ptr(), buf.numel()
 
 
-_WORKSPACE = _Workspace()
+_LIM_WORKSPACE = _Workspace()   # fused_li_manage(_mtp)
+_ATTN_WORKSPACE = _Workspace()  # the attention entry points
 
 
 def _stream_of(t: torch.Tensor) -> int:
@@ -141,7 +142,7 @@ def _fused_li_manage(query, index_weights, index_key_cache, index_block_table, n
     nbytes = _L.nvdsa_fused_li_manage_workspace_size(query.shape[0] if query.dim() else 0,
                                                      index_block_table.shape[-1] * 128 if index_block_table.dim() == 2 else 0,
                                                      query.shape[1] if query.dim() > 1 else 0)
-    ws, wsn = _WORKSPACE.get(query.device, nbytes)
+    ws, wsn = _LIM_WORKSPACE.get(query.device, nbytes)
     _lib.check(_L.nvdsa_fused_li_manage(*map(_ref, descs), ws, wsn, _stream_of(query)))
 
 
@@ -155,7 +156,7 @@ def _fused_li_manage_mtp(query, index_weights, index_key_cache, index_block_tabl
     nbytes = _L.nvdsa_fused_li_manage_mtp_workspace_size(
         batch, index_block_table.shape[-1] * 128 if index_block_table.dim() == 2 else 0,
         query.shape[1] if query.dim() > 1 else 0)
-    ws, wsn = _WORKSPACE.get(query.device, nbytes)
+    ws, wsn = _LIM_WORKSPACE.get(query.device, nbytes)
     _lib.check(_L.nvdsa_fused_li_manage_mtp(*map(_ref, descs), ws, wsn, _stream_of(query)))
 
 
@@ -170,7 +171,7 @@ def _attention_workspace(query: torch.Tensor) -> tuple[int, int]:
     rows = query.shape[0] if query.dim() == 3 else 0
     heads = query.shape[1] if query.dim() == 3 else 0
     nbytes = _L.nvdsa_sparse_tail_attention_workspace_size(rows, heads, 0)
-    return _WORKSPACE.get(query.device, nbytes)
+    return _ATTN_WORKSPACE.get(query.device, nbytes)
 
 
 def _sparse_tail_attention(query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv, num_cache_tokens,
@@ -219,6 +220,28 @@ def _fused_copy_sfa_mtp(query_rope, query, actual_seq_lengths_query, actual_seq_
     ws, wsn = _attention_workspace(query)
     _lib.check(_L.nvdsa_fused_copy_sfa_mtp(*map(_ref, descs), float(scale_value), _ref(out), ws, wsn,
                                            _stream_of(query)))
+
+
+def lidu_init_row(query, weights, index_cache, index_block_table, candidate_len, cache_tokens, cache_slots_row,
+                  hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table, block_size) -> None:
+    """nvdsa_initialize_lidu_row on the current stream (no host sync)."""
+    descs = [_D(t) for t in (query, weights, index_cache, index_block_table)]
+    rest = [_D(t) for t in (cache_slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table,
+                            dram_block_table)]
+    nbytes = _L.nvdsa_initialize_lidu_row_workspace_size(cache_slots_row.shape[0] if cache_slots_row.dim() else 0)
+    ws, wsn = _LIM_WORKSPACE.get(query.device, nbytes)
+    _lib.check(_L.nvdsa_initialize_lidu_row(*map(_ref, descs), int(candidate_len), int(cache_tokens),
+                                            *map(_ref, rest), int(block_size), ws, wsn, _stream_of(query)))
+
+
+def lidu_init_row_shared(cache_slots_row, cache_tokens, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table,
+                         dram_block_table) -> None:
+    """nvdsa_initialize_lidu_row_shared (synchronises the current stream once)."""
+    descs = [_D(t) for t in (hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table)]
+    nbytes = _L.nvdsa_initialize_lidu_row_workspace_size(cache_slots_row.shape[0] if cache_slots_row.dim() else 0)
+    ws, wsn = _LIM_WORKSPACE.get(hbm_kpe.device, nbytes)
+    _lib.check(_L.nvdsa_initialize_lidu_row_shared(_ref(_D(cache_slots_row)), int(cache_tokens), *map(_ref, descs),
+                                                   ws, wsn, _stream_of(hbm_kpe)))
 
 
 IMPLS = {

@@ -22,7 +22,9 @@ It restates, in numpy, the semantics of the seven reference operators:
   ut_ops/test_sparse_tail_attention_mtp.py:314-327,
   ops/sparse_tail_attention/op_kernel/nanovllm_sparse_tail_attention_kernel_mla.h:325-353;
 * ``fused_copy_sfa(_mtp)`` — the composition scatter_copy -> attention
-  (ut_ops/test_fused_copy_sfa.py:453-497, README_ops.md:99-141).
+  (ut_ops/test_fused_copy_sfa.py:453-497, README_ops.md:99-141);
+* ``initialize_lidu_row(_shared)`` — the first-decode top-C initialisation
+  and its IndexShare copy (nanovllm/models/dsa_offload_ops.py:251-411).
 
 Where the reference leaves a choice implementation-defined (victim choice —
 a hash-seeded partial scan in fused_li_manage_service_vector.h:72-81,
@@ -323,6 +325,69 @@ def scatter_copy(src_ids, dst_slots, copy_counts, hbm_table, dram_table, hbm_kpe
                 continue
             hc[dr] = dc[sr]
             hk[dr] = dk[sr]
+
+
+# --------------------------------------------------------------------------
+# first-decode LIDU initialisation (reference nanovllm/models/dsa_offload_ops.py:251-411)
+def linear_index_scores(query: np.ndarray, weights: np.ndarray, keys: np.ndarray) -> np.ndarray:
+    """s[t] = sum_h w[h] * (q[h] . k[t]) in float64 -- the initialisation
+    score has no ReLU (dsa_offload_ops.py:306-311)."""
+    q = np.asarray(query, np.float64).reshape(-1, IDX)
+    w = np.asarray(weights, np.float64).reshape(-1)
+    return (np.asarray(keys, np.float64) @ q.T) @ w
+
+
+def _lidu_init_checks(candidate_len: int, cache_tokens: int, block_size: int = BLOCK) -> None:
+    """The reference's argument errors (dsa_offload_ops.py:280-294)."""
+    if cache_tokens < TOPK:
+        raise ValueError(f"LIDU nonzero cache budget must be >= {TOPK}, got {cache_tokens}.")
+    if candidate_len < cache_tokens:
+        raise ValueError(f"LIDU cache budget {cache_tokens} exceeds source length {candidate_len}.")
+    if candidate_len % int(block_size):
+        raise ValueError("LIDU source must consist only of complete blocks.")
+
+
+def initialize_lidu_row(query, weights, key_cache, index_table_row, candidate_len: int, cache_tokens: int,
+                        slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_table_row, dram_table_row,
+                        dtype: str = "bf16"):
+    """Top-C of the linear scores over tokens [0, candidate_len) (ties to the
+    lower token), slot i given to the i-th smallest selected token, every
+    other entry of the pool row set to -1, and the C rows copied DRAM -> HBM
+    (dsa_offload_ops.py:251-360).  The reference assigns slots in the order
+    torch.topk(sorted=False) returns the tokens, which is implementation-
+    defined; ascending token order is this build's canonical choice.
+    Mutates slots_row and the HBM caches; returns (source_ids, slots) or
+    None when cache_tokens <= 0."""
+    n, c = int(candidate_len), int(cache_tokens)
+    if c <= 0:
+        return None
+    _lidu_init_checks(n, c)
+    keys = gather_rows(bits_to_f32(key_cache, dtype), np.asarray(index_table_row), n)
+    scores = linear_index_scores(bits_to_f32(query, dtype), bits_to_f32(weights, dtype), keys)
+    sel = np.nonzero(topk_mask(scores, c))[0].astype(np.int32)
+    slots = np.arange(c, dtype=np.int32)
+    slots_row[:] = -1
+    slots_row[sel] = slots
+    scatter_copy(sel[None, :], slots[None, :], np.array([c], np.int32), np.asarray(hbm_table_row)[None],
+                 np.asarray(dram_table_row)[None], hbm_kpe, hbm_ckv, dram_kpe, dram_ckv)
+    return sel, slots
+
+
+def initialize_lidu_row_shared(slots_row, cache_tokens: int, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_table_row,
+                               dram_table_row):
+    """A shared IndexShare layer: copy this layer's DRAM rows of every token
+    the owner's pool row caches (ascending token) to its slot
+    (dsa_offload_ops.py:363-411).  Returns (source_ids, slots) or None."""
+    c = int(cache_tokens)
+    if c <= 0:
+        return None
+    src = np.nonzero(np.asarray(slots_row) >= 0)[0].astype(np.int32)
+    dst = np.asarray(slots_row)[src].astype(np.int32)
+    if src.size != c:
+        raise RuntimeError(f"Shared layer LIDU initialization found {src.size} cached tokens, expected {c}.")
+    scatter_copy(src[None, :], dst[None, :], np.array([c], np.int32), np.asarray(hbm_table_row)[None],
+                 np.asarray(dram_table_row)[None], hbm_kpe, hbm_ckv, dram_kpe, dram_ckv)
+    return src, dst
 
 
 # --------------------------------------------------------------------------
