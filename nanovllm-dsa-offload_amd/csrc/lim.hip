@@ -46,7 +46,8 @@ constexpr int kDigitBits = 13;                    // radix digit width
 constexpr int kBins = 1 << kDigitBits;            // radix histogram bins
 constexpr int kBinsPerThread = kBins / kManageThreads;
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
-constexpr int kLdsSlots = 4096;  // cache budgets up to this keep their slot tables in LDS
+constexpr int kLdsSlots = 4096;     // MTP0: cache budgets up to this keep their slot tables in LDS
+constexpr int kLdsSlotsMtp = 8192;  // MTP3 (its LDS holds no register-resident candidates)
 constexpr uint32_t kStateShift = 24;
 constexpr uint32_t kStateFree = 0;
 constexpr uint32_t kStateHit = 1;
@@ -60,6 +61,7 @@ struct LimWs {
   uint32_t* slot_table; // [B, 16384] token | state << 24
   uint32_t* slot_key;   // [B, 16384] score key of candidate slots
   int32_t* miss_list;   // [B, 8192]
+  uint32_t* select;     // [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq (threshold kernel)
   uint8_t* masks;       // [B, S_cap] per-token query mask (MTP)
 };
 
@@ -74,6 +76,8 @@ LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
   p += align256(sizeof(uint32_t) * batch * kSlotStride);
   w.miss_list = reinterpret_cast<int32_t*>(p);
   p += align256(sizeof(int32_t) * batch * kUnionCap);
+  w.select = reinterpret_cast<uint32_t*>(p);
+  p += align256(sizeof(uint32_t) * 4 * batch * queries);
   w.masks = queries > 1 ? reinterpret_cast<uint8_t*>(p) : nullptr;
   return w;
 }
@@ -519,6 +523,100 @@ __device__ __forceinline__ int select_victims(int c, int m, const uint32_t* stab
 }
 
 // ---------------------------------------------------------------------------
+// Top-2048 threshold of one (request, query) score row, written to the
+// workspace for a management kernel (MTP3, and MTP0 sources longer than the
+// manage kernel keeps in registers).  One workgroup per row; RES > 0 keeps
+// the row's keys in registers (RES chunks of 4096 tokens) for its radix
+// passes, RES == 0 streams them.
+template <int RES>
+__global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a, LimWs w, int queries) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  const int b = blockIdx.x / queries;
+  const int q = blockIdx.x - b * queries;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  const bool valid = queries > 1 ? lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)
+                                 : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
+  if (!valid) return;
+  const int64_t cap = a.source_capacity;
+  const float* s = w.scores + (static_cast<int64_t>(b) * queries + q) * cap;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  SelectOut sel;
+  if constexpr (RES > 0) {
+    uint32_t u[RES][kItems];
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch) {  // all loads first (redirected past cap, ignored: t >= n)
+      const int t0 = ch * kChunk + tid * kItems;
+      const int64_t tl = t0 < cap ? t0 : cap - kItems;
+      const uint4 x = *reinterpret_cast<const uint4*>(s + tl);
+      const uint4 y = *reinterpret_cast<const uint4*>(s + tl + 4);
+      u[ch][0] = x.x; u[ch][1] = x.y; u[ch][2] = x.z; u[ch][3] = x.w;
+      u[ch][4] = y.x; u[ch][5] = y.y; u[ch][6] = y.z; u[ch][7] = y.w;
+    }
+    uint32_t lo = 0xffffffffu, hi = 0u;
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch)
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) {
+        u[ch][e] = score_key(__uint_as_float(u[ch][e]));
+        if (ch * kChunk + tid * kItems + e < n) {
+          lo = min(lo, u[ch][e]);
+          hi = max(hi, u[ch][e]);
+        }
+      }
+    block_minmax(lo, hi, red);
+    sel = radix_select_visit(
+        kTopK, lo, hi,
+        [&](auto&& fn) {
+#pragma unroll
+          for (int ch = 0; ch < RES; ++ch)
+#pragma unroll
+            for (int e = 0; e < kItems; ++e)
+              if (ch * kChunk + tid * kItems + e < n) fn(u[ch][e]);
+        },
+        hist, scratch, bcast);
+  } else {
+    const int ngroups = static_cast<int>(ceil_div(n, 4));
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int g = tid; g < ngroups; g += kManageThreads) {
+      uint32_t key[4];
+      bool inc[4];
+      load_score_keys(s, n, 4 * g, key, inc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (inc[e]) {
+          lo = min(lo, key[e]);
+          hi = max(hi, key[e]);
+        }
+    }
+    block_minmax(lo, hi, red);
+    sel = radix_select(
+        ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); },
+        hist, scratch, bcast);
+  }
+  if (tid == 0) {
+    uint32_t* out = w.select + (static_cast<int64_t>(b) * queries + q) * 4;
+    out[0] = sel.thresh;
+    out[1] = static_cast<uint32_t>(sel.need_eq);
+    out[2] = static_cast<uint32_t>(sel.cnt_eq);
+  }
+}
+
+// The threshold of score row `row`, read as wave-uniform values (call with a
+// row index that is the same across the wave).
+__device__ inline SelectOut read_select(const LimWs& w, int64_t row) {
+  const uint32_t* p = w.select + row * 4;
+  return SelectOut{static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(p[0])),
+                   static_cast<int>(__builtin_amdgcn_readfirstlane(p[1])),
+                   static_cast<int>(__builtin_amdgcn_readfirstlane(p[2]))};
+}
+
+// ---------------------------------------------------------------------------
 // 2a. MTP0 management.
 
 // Classify eight consecutive candidates [t0, t0 + 8) of the ordered pass:
@@ -684,31 +782,26 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
     // redirected to the last group and ignored (t0 >= cap >= n).  So every
     // load is unconditional, and all 32 of a thread's loads are in flight
     // together.
-    uint4 raw_s[RES][2];
-    int4 raw_p[RES][2];
+    int32_t pr[RES][kItems];
 #pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {  // all loads first ...
+    for (int ch = 0; ch < RES; ++ch) {  // all loads first (raw bits straight into u / pr) ...
       const int t0 = ch * kChunk + tid * kItems;
       const int64_t tl = t0 < cap ? t0 : cap - kItems;
-      raw_s[ch][0] = *reinterpret_cast<const uint4*>(s + tl);
-      raw_s[ch][1] = *reinterpret_cast<const uint4*>(s + tl + 4);
-      raw_p[ch][0] = *reinterpret_cast<const int4*>(pool + tl);
-      raw_p[ch][1] = *reinterpret_cast<const int4*>(pool + tl + 4);
+      const uint4 x = *reinterpret_cast<const uint4*>(s + tl);
+      const uint4 y = *reinterpret_cast<const uint4*>(s + tl + 4);
+      const int4 pa = *reinterpret_cast<const int4*>(pool + tl);
+      const int4 pb = *reinterpret_cast<const int4*>(pool + tl + 4);
+      u[ch][0] = x.x; u[ch][1] = x.y; u[ch][2] = x.z; u[ch][3] = x.w;
+      u[ch][4] = y.x; u[ch][5] = y.y; u[ch][6] = y.z; u[ch][7] = y.w;
+      pr[ch][0] = pa.x; pr[ch][1] = pa.y; pr[ch][2] = pa.z; pr[ch][3] = pa.w;
+      pr[ch][4] = pb.x; pr[ch][5] = pb.y; pr[ch][6] = pb.z; pr[ch][7] = pb.w;
     }
 #pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {  // ... then the conversions
-      const uint32_t xs[kItems] = {raw_s[ch][0].x, raw_s[ch][0].y, raw_s[ch][0].z, raw_s[ch][0].w,
-                                   raw_s[ch][1].x, raw_s[ch][1].y, raw_s[ch][1].z, raw_s[ch][1].w};
-      const int32_t ps[kItems] = {raw_p[ch][0].x, raw_p[ch][0].y, raw_p[ch][0].z, raw_p[ch][0].w,
-                                  raw_p[ch][1].x, raw_p[ch][1].y, raw_p[ch][1].z, raw_p[ch][1].w};
-      uint32_t pv[kItems];
+    for (int ch = 0; ch < RES; ++ch) {  // ... then the conversions, in place
 #pragma unroll
-      for (int e = 0; e < kItems; ++e) {
-        u[ch][e] = score_key(__uint_as_float(xs[e]));
-        pv[e] = p16(ps[e]);
-      }
+      for (int e = 0; e < kItems; ++e) u[ch][e] = score_key(__uint_as_float(u[ch][e]));
 #pragma unroll
-      for (int e = 0; e < kItems / 2; ++e) pk[ch][e] = pv[2 * e] | (pv[2 * e + 1] << 16);
+      for (int e = 0; e < kItems / 2; ++e) pk[ch][e] = p16(pr[ch][2 * e]) | (p16(pr[ch][2 * e + 1]) << 16);
     }
     uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
@@ -720,8 +813,21 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
           hi = max(hi, u[ch][e]);
         }
     block_minmax(lo, hi, red);
+    // Keys relative to the minimum, in place (no per-pass key - kmin copies
+    // for the compiler to keep in registers); the threshold comes back in the
+    // same frame, so the classification compares like with like.
+#pragma unroll
+    for (int ch = 0; ch < RES; ++ch)
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) {
+        u[ch][e] -= lo;
+        // Opaque to the optimiser: otherwise it folds the subtraction into
+        // the later compares and keeps both the absolute and the relative
+        // keys live (spilling).  Emits no instruction.
+        asm volatile("" : "+v"(u[ch][e]));
+      }
     const SelectOut sel = radix_select_visit(
-        kTopK, lo, hi,
+        kTopK, 0u, hi - lo,
         [&](auto&& fn) {
 #pragma unroll
           for (int ch = 0; ch < RES; ++ch)
@@ -785,30 +891,14 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
             stab[slot] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
           } else {
             stab[slot] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
-            skey[slot] = u[ch][e];
+            skey[slot] = u[ch][e] + lo;  // absolute key (free slots rank below every score)
           }
         }
       }
       miss_run += lane16x8(tot, ch);
     }
   } else {
-    const int ngroups = static_cast<int>(ceil_div(n, 4));
-    uint32_t lo = 0xffffffffu, hi = 0u;
-    for (int g = tid; g < ngroups; g += kManageThreads) {
-      uint32_t key[4];
-      bool inc[4];
-      load_score_keys(s, n, 4 * g, key, inc);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (inc[e]) {
-          lo = min(lo, key[e]);
-          hi = max(hi, key[e]);
-        }
-    }
-    block_minmax(lo, hi, red);
-    const SelectOut sel = radix_select(
-        ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); },
-        hist, scratch, bcast);
+    const SelectOut sel = read_select(w, b);  // lim_threshold_kernel
     const bool need_rank = sel.cnt_eq != sel.need_eq;
     for (int base = 0; base < n; base += kChunk) {
       const int t0 = base + tid * kItems;
@@ -832,8 +922,8 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kUnionCap];
-  __shared__ uint32_t lds_stab[kLdsSlots];
-  __shared__ uint32_t lds_skey[kLdsSlots];
+  __shared__ uint32_t lds_stab[kLdsSlotsMtp];
+  __shared__ uint32_t lds_skey[kLdsSlotsMtp];
   __shared__ uint32_t thr[kMtpQueries];
   __shared__ int need[kMtpQueries];
   __shared__ int rank_needed[kMtpQueries];
@@ -849,7 +939,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + static_cast<int64_t>(b) * kMtpQueries * cap;
   int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  const bool lds_tables = c <= kLdsSlots;
+  const bool lds_tables = c <= kLdsSlotsMtp;
   uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kSlotStride;
   uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kSlotStride;
   uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
@@ -859,29 +949,11 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  for (int q = 0; q < kMtpQueries; ++q) {
-    const float* sq = s + q * cap;
-    uint32_t lo = 0xffffffffu, hi = 0u;
-    for (int g = tid; g < ngroups; g += kManageThreads) {
-      uint32_t key[4];
-      bool inc[4];
-      load_score_keys(sq, n, 4 * g, key, inc);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (inc[e]) {
-          lo = min(lo, key[e]);
-          hi = max(hi, key[e]);
-        }
-    }
-    block_minmax(lo, hi, red);
-    const SelectOut sel = radix_select(
-        ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(sq, n, 4 * g, key, inc); },
-        hist, scratch, bcast);
-    if (tid == 0) {
-      thr[q] = sel.thresh;
-      need[q] = sel.need_eq;
-      rank_needed[q] = sel.cnt_eq != sel.need_eq;
-    }
+  if (tid < kMtpQueries) {  // per-query thresholds from lim_threshold_kernel (one lane each)
+    const uint32_t* sp = w.select + (static_cast<int64_t>(b) * kMtpQueries + tid) * 4;
+    thr[tid] = sp[0];
+    need[tid] = static_cast<int>(sp[1]);
+    rank_needed[tid] = sp[2] != sp[1];
   }
   __syncthreads();
   const bool any_rank = rank_needed[0] | rank_needed[1] | rank_needed[2] | rank_needed[3];
@@ -1244,10 +1316,21 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 mgrid(static_cast<uint32_t>(a.batch)), mblock(kManageThreads);
+  if (Q == 1 && a.source_capacity <= 8 * kChunk) {  // one kernel, candidates in registers
+    launch_kernel(kKernLimManage, lim_manage_kernel<8>, mgrid, mblock, stream, a, w);
+    return hipGetLastError();
+  }
+  // Thresholds first, one workgroup per (request, query) score row.
+  const dim3 tgrid(static_cast<uint32_t>(a.batch * Q));
+  if (a.source_capacity <= 16 * kChunk) {
+    launch_kernel(kKernLimThreshold, lim_threshold_kernel<16>, tgrid, mblock, stream, a, w, Q);
+  } else {
+    launch_kernel(kKernLimThreshold, lim_threshold_kernel<0>, tgrid, mblock, stream, a, w, Q);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
   if (Q > 1) {
     launch_kernel(kKernLimManageMtp, lim_manage_mtp_kernel, mgrid, mblock, stream, a, w);
-  } else if (a.source_capacity <= 8 * kChunk) {
-    launch_kernel(kKernLimManage, lim_manage_kernel<8>, mgrid, mblock, stream, a, w);
   } else {
     launch_kernel(kKernLimManage, lim_manage_kernel<0>, mgrid, mblock, stream, a, w);
   }
@@ -1260,6 +1343,7 @@ size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries) 
   size_t total = align256(sizeof(float) * batch * queries * source_capacity);
   total += 2 * align256(sizeof(uint32_t) * batch * kSlotStride);
   total += align256(sizeof(int32_t) * batch * kUnionCap);
+  total += align256(sizeof(uint32_t) * 4 * batch * queries);
   if (queries > 1) total += align256(static_cast<size_t>(batch) * source_capacity);
   return total;
 }

@@ -22,7 +22,8 @@ enum KernelId : int {
   kKernSfaCombine = 6,
   kKernLiduInit = 7,
   kKernLiduShared = 8,
-  kKernCount = 9
+  kKernLimThreshold = 9,
+  kKernCount = 10
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.
@@ -160,7 +161,6 @@ struct SfaArgs {
   const void* dram_ckv;
   int64_t dram_cols;
   int64_t dram_blocks;
-  int miss_splits;              // fused: splits per row reserved for the miss tiles (set by the launcher)
   void* workspace;
   size_t workspace_bytes;
 };

@@ -21,11 +21,12 @@
 //   rounding stays at fp32 level.  A second kernel merges the per-split
 //   (max, sum, numerator) partials.
 //   fused_copy_sfa (MTP0): a row's miss keys are the first miss_counts
-//   entries of its list.  The first kMissSplitPct percent of a row's splits
-//   take the tiles holding them: each such tile is read once from host-mapped
-//   DRAM, stored to its HBM slots and consumed from LDS.  The other splits
-//   take the HBM-only tiles, so the host-link-bound copy and the HBM-bound
-//   attention run side by side.  fused_copy_sfa_mtp: the union misses are
+//   entries of its list.  The first kMissSplits splits of the row take the
+//   tiles holding them: each such tile is read once from host-mapped DRAM,
+//   stored to its HBM slots and consumed from LDS.  A split's host tiles are
+//   sequential (one PCIe round trip each).  The other splits take the
+//   HBM-only tiles, so the host-link-bound copy and the HBM-bound attention
+//   run side by side.  fused_copy_sfa_mtp: the union misses are
 //   not tile-aligned to any one query row, so the union is copied first
 //   (scatter_copy) and the MTP attention follows on the same stream.
 #include <cfloat>
@@ -48,7 +49,7 @@ constexpr int kMaxSplits = 64;
 constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per window (one key per thread)
 constexpr int kWindowKeys = kWindowTiles * kTileKeys;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMissSplitPct = 20;  // fused: share of a row's splits given the host-sourced tiles
+constexpr int kMissSplits = 2;  // fused: splits of a row that take its host-sourced tiles
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -147,9 +148,11 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   // host-link-bound copies and the HBM-bound tiles proceed side by side
   // instead of every workgroup first stalling on its share of the copy.
   int t_first = split, t_stride = splits, t_end = ntiles;
-  if (FUSED) {
-    const int miss_splits = a.miss_splits;
-    const int mtiles = static_cast<int>(ceil_div(copy_count, kTileKeys));
+  const int mtiles = FUSED ? static_cast<int>(ceil_div(copy_count, kTileKeys)) : 0;
+  if (FUSED && mtiles > 0 && splits >= 2) {  // (one split per row takes every tile)
+    // Two splits take the host-sourced tiles (measured best at cfg1; more
+    // of them leave too few splits for the row's HBM-resident tiles).
+    const int miss_splits = kMissSplits < splits - 1 ? kMissSplits : splits - 1;
     if (split < miss_splits) {
       t_first = split;
       t_stride = miss_splits;
@@ -433,8 +436,6 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int splits = choose_splits(rows, hgroups);
   SfaArgs args = a;
   // Fused: ~30% of a row's splits handle the host-sourced miss tiles.
-  args.miss_splits = FUSED ? (splits >= 2 ? (splits * kMissSplitPct + 99) / 100 : 0) : 0;
-  if (FUSED && args.miss_splits >= splits) args.miss_splits = splits - 1;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
   launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED>,
                 dim3(static_cast<uint32_t>(rows * splits), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads),
