@@ -173,20 +173,32 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
     return;
   }
 
-  // Query rows of the block's heads -> LDS (zeros beyond H or for inactive rows).
-  {
+  // Query rows of the block's heads -> LDS (zeros beyond H or for inactive
+  // rows): all 18 loads of a thread in flight together, then the stores.
+  auto stage_queries = [&]() {
+    constexpr int kPer = kHeadsPerBlock * kChunksPerKey / kAttnThreads;  // 18
+    static_assert(kPer * kAttnThreads == kHeadsPerBlock * kChunksPerKey, "query staging");
     const uint4* qn = static_cast<const uint4*>(a.query);
     const uint4* qr = static_cast<const uint4*>(a.query_rope);
-    for (int i = tid; i < kHeadsPerBlock * kChunksPerKey; i += kAttnThreads) {
+    uint4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * kAttnThreads + tid;
       const int hh = i / kChunksPerKey;
       const int c = i - hh * kChunksPerKey;
       const int hgl = hg * kHeadsPerBlock + hh;
-      uint4 v = make_uint4(0, 0, 0, 0);
+      v[k] = make_uint4(0, 0, 0, 0);
       if (plan.active && hgl < a.heads)
-        v = c < 64 ? qn[(row * H + hgl) * 64 + c] : qr[(row * H + hgl) * 8 + (c - 64)];
-      *reinterpret_cast<uint4*>(&qs[hh * kQStride + c * 8]) = v;
+        v[k] = c < 64 ? qn[(row * H + hgl) * 64 + c] : qr[(row * H + hgl) * 8 + (c - 64)];
     }
-  }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * kAttnThreads + tid;
+      const int hh = i / kChunksPerKey;
+      const int c = i - hh * kChunksPerKey;
+      *reinterpret_cast<uint4*>(&qs[hh * kQStride + c * 8]) = v[k];
+    }
+  };
 
   const int32_t* topk = a.topk_dst + row * kTopK;
   const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
@@ -272,6 +284,14 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
     }
   };
 
+  // The first tile's loads (possibly host rows) are issued before the
+  // queries are staged; the barrier after its store publishes both.
+  uint4 pf[kChunksPerThread];
+  resolve_window(0);
+  __syncthreads();
+  load_tile(0, pf);
+  stage_queries();
+
   const float qscale = a.scale * kLog2e;
   float m_run = -INFINITY;  // running max (base-2 logits) of head `head`
   float l_run = 0.f;        // this lane's share of the running sum
@@ -279,12 +299,13 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
 #pragma unroll
   for (int i = 0; i < kCkvDim / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint4 pf[kChunksPerThread];
   for (int first = 0; first < my_tiles; first += kWindowTiles) {
-    resolve_window(first);
-    __syncthreads();
+    if (first > 0) {
+      resolve_window(first);
+      __syncthreads();
+      load_tile(0, pf);
+    }
     const int wtiles = min(kWindowTiles, my_tiles - first);
-    load_tile(0, pf);
     for (int w = 0; w < wtiles; ++w) {
       store_tile(w, pf);
       __syncthreads();                     // tile w resident in LDS
