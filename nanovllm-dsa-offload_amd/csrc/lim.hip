@@ -41,6 +41,7 @@ namespace {
 
 constexpr int kScoreWaves = 4;                  // waves per score workgroup
 constexpr int kQStride = kIndexDim + 8;         // padded LDS row (bank spread)
+constexpr int kStageStride = 17;                // 16-byte chunks per staged key row (16 + 1 pad)
 constexpr int kManageThreads = 512;
 constexpr int kDigitBits = 13;                    // radix digit width
 constexpr int kBins = 1 << kDigitBits;            // radix histogram bins
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
                                                                         int fixed_n) {
   __shared__ uint16_t qs[Q * HEADS * kQStride];
   __shared__ float ws[Q * HEADS];
+  __shared__ uint4 kstage[kScoreWaves * 32 * kStageStride];
   const int b = blockIdx.y;
   int n = fixed_n;
   if (fixed_n < 0) {
@@ -144,13 +146,29 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
         if (t0 + j < n) srow[q * cap + t0 + j] = -FLT_MAX;
     return;
   }
-  // Key tile: 4 token tiles x 8 k-steps, 16 bytes each, all loads issued first.
+  // Key block (128 rows of 256 bytes): each load instruction reads 4 whole
+  // rows (16 lanes per row), all 32 issued first.  (Loading the MFMA operand
+  // layout directly -- 32 rows x 32 bytes per instruction -- has the L2 fetch
+  // ~1.4x the block's bytes from HBM.)
   const uint4* kp = static_cast<const uint4*>(a.key_cache) + static_cast<int64_t>(phys) * kBlock * 16;
+  uint4 raw[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) raw[i] = kp[i * kWave + lane];  // row 4i + lane/16, chunk lane%16
+  // Per 32-token tile, a transpose through the wave's own LDS rows into the
+  // operand layout: kb[tt][ks] = chunk 2ks+grp of row 32tt+col_lane.  Only
+  // this wave touches these rows.  A wave's LDS operations are performed in
+  // its execution order, and the stores and loads below may alias, so the
+  // compiler keeps their program order; no fence is needed (one here keeps
+  // `raw` in scratch memory).
+  uint4* st = kstage + wave * 32 * kStageStride;
   uint4 kb[4][8];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
+  for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kb[tt][ks] = kp[(tt * 32 + col_lane) * 16 + ks * 2 + grp];
+    for (int j = 0; j < 8; ++j) st[(4 * j + (lane >> 4)) * kStageStride + (lane & 15)] = raw[tt * 8 + j];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kb[tt][ks] = st[col_lane * kStageStride + ks * 2 + grp];
+  }
 
 #pragma unroll 1
   for (int q = 0; q < Q; ++q) {
