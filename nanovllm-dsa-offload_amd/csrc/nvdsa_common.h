@@ -45,6 +45,14 @@ struct Bf16 {
     u += 0x7fffu + ((u >> 16) & 1u);
     return static_cast<uint16_t>(u >> 16);
   }
+  // Round-to-nearest-even for finite values (no NaN check).
+  __device__ static inline uint16_t from_finite(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+  }
+  // Leading part of a hi + lo split: truncation (the lo part takes the rest).
+  __device__ static inline uint16_t hi_part(float f) { return static_cast<uint16_t>(__float_as_uint(f) >> 16); }
   __device__ static inline f32x16_t mfma32(vec8 a, vec8 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -63,6 +71,8 @@ struct F16 {
     _Float16 h = static_cast<_Float16>(f);
     return __builtin_bit_cast(uint16_t, h);
   }
+  __device__ static inline uint16_t from_finite(float f) { return from_float(f); }
+  __device__ static inline uint16_t hi_part(float f) { return from_float(f); }
   __device__ static inline f32x16_t mfma32(vec8 a, vec8 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }

@@ -13,13 +13,16 @@
 // Kernel design (split-KV flash decode):
 //   grid = rows x splits x ceil(heads/64); a 256-thread workgroup owns one
 //   row, one split of its key list and 64 heads (16 heads per wavefront).
-//   Keys are processed in tiles of 32.  The block's 64x576 queries are
-//   staged in LDS once; each tile is gathered row-contiguous into LDS
-//   (conflict-free 16-byte MFMA operand reads).  S^T = K . Q^T and
+//   Keys are processed in tiles of 32.  Each lane keeps its query operand
+//   (one head, 18 x 16 bytes of the 576 dims) in registers for the whole
+//   split; each tile is gathered row-contiguous into LDS (conflict-free
+//   16-byte operand reads for S; the V^T operand of the PV product comes
+//   from transposing ds_read_b64_tr_b16 reads).  S^T = K . Q^T and
 //   O^T = V^T . P^T run on v_mfma_f32_16x16x32; the online softmax is in
-//   base 2, and P enters the PV product as a bf16/f16 hi+lo pair so its
-//   rounding stays at fp32 level.  A second kernel merges the per-split
-//   (max, sum, numerator) partials.
+//   base 2 with a running max that moves only when exceeded by more than
+//   kMaxSlack (few numerator rescales), and P enters the PV product as a
+//   bf16/f16 hi+lo pair so its rounding stays at fp32 level.  A second
+//   kernel merges the per-split (max, sum, numerator) partials.
 //   fused_copy_sfa (MTP0): a row's miss keys are the first miss_counts
 //   entries of its list.  The first kMissSplits splits of the row take the
 //   tiles holding them: each such tile is read once from host-mapped DRAM,
@@ -49,9 +52,20 @@ constexpr int kMaxSplits = 64;
 constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per window (one key per thread)
 constexpr int kWindowKeys = kWindowTiles * kTileKeys;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kMaxSlack = 8.f;  // base-2 headroom of the running max (P < 256)
 constexpr int kMissSplits = 2;  // fused: splits of a row that take its host-sourced tiles
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i reads four
+// 16-bit values M[i][0..3] at its address; lane l receives
+// M[4j + (l >> 2)][l & 3] for j = 0..3.
+__device__ inline uint2 lds_read_tr16(const uint16_t* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(uint2, v);
+}
 
 struct RowPlan {
   int active;      // 1 when the row attends
@@ -110,7 +124,6 @@ int choose_splits(int64_t rows, int64_t head_groups) {
 
 template <typename T, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Partials part, int splits) {
-  __shared__ uint16_t qs[kHeadsPerBlock * kQStride];  // the block's 64 query rows (576 each)
   __shared__ uint16_t ks[kTileKeys * kKStride];       // key tile, row-major
   // Resolved keys of the current window of kWindowTiles tiles (one per thread):
   // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to, flags.
@@ -173,30 +186,19 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
     return;
   }
 
-  // Query rows of the block's heads -> LDS (zeros beyond H or for inactive
-  // rows): all 18 loads of a thread in flight together, then the stores.
-  auto stage_queries = [&]() {
-    constexpr int kPer = kHeadsPerBlock * kChunksPerKey / kAttnThreads;  // 18
-    static_assert(kPer * kAttnThreads == kHeadsPerBlock * kChunksPerKey, "query staging");
-    const uint4* qn = static_cast<const uint4*>(a.query);
-    const uint4* qr = static_cast<const uint4*>(a.query_rope);
-    uint4 v[kPer];
+  // Query operand of this lane, kept in registers for the whole split:
+  // head `head`, dims 32kk + 8g .. +7 (16-byte chunk 4kk + g of the 576),
+  // zeros for heads beyond H and inactive rows.
+  uint4 qreg[kQkDim / 32];
+  auto load_queries = [&]() {
+    const uint4* qn = static_cast<const uint4*>(a.query) + (row * H + head) * 64;
+    const uint4* qr = static_cast<const uint4*>(a.query_rope) + (row * H + head) * 8;
+    const bool ok = plan.active && wave_active && head < a.heads;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = k * kAttnThreads + tid;
-      const int hh = i / kChunksPerKey;
-      const int c = i - hh * kChunksPerKey;
-      const int hgl = hg * kHeadsPerBlock + hh;
-      v[k] = make_uint4(0, 0, 0, 0);
-      if (plan.active && hgl < a.heads)
-        v[k] = c < 64 ? qn[(row * H + hgl) * 64 + c] : qr[(row * H + hgl) * 8 + (c - 64)];
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = k * kAttnThreads + tid;
-      const int hh = i / kChunksPerKey;
-      const int c = i - hh * kChunksPerKey;
-      *reinterpret_cast<uint4*>(&qs[hh * kQStride + c * 8]) = v[k];
+    for (int kk = 0; kk < kQkDim / 32; ++kk) {
+      const int c = 4 * kk + g;
+      qreg[kk] = make_uint4(0, 0, 0, 0);
+      if (ok) qreg[kk] = c < 64 ? qn[c] : qr[c - 64];
     }
   };
 
@@ -247,9 +249,11 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   // consecutive lanes read consecutive 16 bytes of one row, so a wave reads
   // whole 1 KiB CKV rows (full-width PCIe requests for host rows).
   auto load_tile = [&](int w, uint4 (&pf)[kChunksPerThread]) {
+    int t = tid;
+    asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
     for (int jj = 0; jj < kChunksPerThread; ++jj) {
-      const int cidx = jj * kAttnThreads + tid;
+      const int cidx = jj * kAttnThreads + t;
       const int k = cidx / kChunksPerKey;
       const int pc = cidx - k * kChunksPerKey;
       const int wk = w * kTileKeys + k;
@@ -265,9 +269,11 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
     }
   };
   auto store_tile = [&](int w, const uint4 (&pf)[kChunksPerThread]) {
+    int t = tid;
+    asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
     for (int jj = 0; jj < kChunksPerThread; ++jj) {
-      const int cidx = jj * kAttnThreads + tid;
+      const int cidx = jj * kAttnThreads + t;
       const int k = cidx / kChunksPerKey;
       const int pc = cidx - k * kChunksPerKey;
       *reinterpret_cast<uint4*>(&ks[k * kKStride + pc * 8]) = pf[jj];
@@ -285,12 +291,12 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   };
 
   // The first tile's loads (possibly host rows) are issued before the
-  // queries are staged; the barrier after its store publishes both.
+  // query loads.
   uint4 pf[kChunksPerThread];
   resolve_window(0);
   __syncthreads();
   load_tile(0, pf);
-  stage_queries();
+  load_queries();
 
   const float qscale = a.scale * kLog2e;
   float m_run = -INFINITY;  // running max (base-2 logits) of head `head`
@@ -314,7 +320,6 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
       if (wave_active && plan.active) {
         // S^T tile: two 16-key blocks; lane holds S[head][kt*16 + 4g + i].
         f32x4_t sacc[2];
-        const uint16_t* qrow = &qs[(wave * 16 + l16) * kQStride + g * 8];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -322,8 +327,7 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
 #pragma unroll
           for (int kk = 0; kk < kQkDim / 32; ++kk) {
             const uint4 kf = *reinterpret_cast<const uint4*>(krow + kk * 32);
-            const uint4 qf = *reinterpret_cast<const uint4*>(qrow + kk * 32);
-            acc = T::mfma16(__builtin_bit_cast(typename T::vec8, kf), __builtin_bit_cast(typename T::vec8, qf), acc);
+            acc = T::mfma16(__builtin_bit_cast(typename T::vec8, kf), __builtin_bit_cast(typename T::vec8, qreg[kk]), acc);
             if ((kk & 5) == 5) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
           }
           sacc[kt] = acc;
@@ -341,21 +345,33 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
           }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
+        // The reference max only moves when the tile max exceeds it by more
+        // than kMaxSlack (base-2 units), so P stays below 2^kMaxSlack and the
+        // numerator is rescaled on few tiles (softmax does not depend on the
+        // subtracted constant).
+        const bool grow = mx > m_run + kMaxSlack;  // also m_run == -inf with a finite tile max
+        const float m_new = grow ? mx : m_run;
         if (m_new != -INFINITY) {
-          const float alpha = exp2f(m_run - m_new);  // m_run == -inf gives 0
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 1 unless grow; 0 from m_run == -inf
+          const bool rescale = __any(grow && m_run != -INFINITY);  // (zero numerators need none)
           m_run = m_new;
           float psum = 0.f;
           float p[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            p[i] = exp2f(sv[i] - m_new);
+            p[i] = __builtin_amdgcn_exp2f(sv[i] - m_new);  // (results below 2^-126 flush to 0)
             psum += p[i];
           }
           l_run = l_run * alpha + psum;
-          // The numerator needs rescaling only when some head's running max
-          // moved in this tile (alpha == 1 exactly otherwise).
-          const bool rescale = __any(alpha != 1.f);
+          if (rescale) {
+#pragma unroll
+            for (int dt = 0; dt < kCkvDim / 16; ++dt) {
+              oacc[dt][0] *= alpha;
+              oacc[dt][1] *= alpha;
+              oacc[dt][2] *= alpha;
+              oacc[dt][3] *= alpha;
+            }
+          }
           // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
           // ~16 mantissa bits of P instead of 8.
           typename T::vec8 pb_hi, pb_lo;
@@ -363,34 +379,29 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
           uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            phs[i] = T::from_float(p[i]);
-            pls[i] = T::from_float(p[i] - T::to_float(phs[i]));
+            phs[i] = T::hi_part(p[i]);
+            pls[i] = T::from_finite(p[i] - T::to_float(phs[i]));
           }
-          // A operand V^T[dim][key] read from the row-major tile: keys
-          // 4g..4g+3 and 16+4g..16+4g+3 (the lanes' S^T columns) at dim
-          // dt*16 + l16.
-          const uint16_t* v0 = &ks[(4 * g) * kKStride + l16];
-          const uint16_t* v1 = &ks[(16 + 4 * g) * kKStride + l16];
+          // A operand V^T[dim][key] from the row-major tile: keys 4g..4g+3
+          // and 16+4g..16+4g+3 (the lanes' S^T columns) at dim dt*16 + l16,
+          // each 4-key group one transposing LDS read (lane i of a 16-lane
+          // group reads dims 4(i&3)..+3 of key i>>2; lane l receives the
+          // four keys' values at dim l).
+          const uint16_t* v0 = &ks[(4 * g + (l16 >> 2)) * kKStride + 4 * (l16 & 3)];
+          const uint16_t* v1 = &ks[(16 + 4 * g + (l16 >> 2)) * kKStride + 4 * (l16 & 3)];
 #pragma unroll
           for (int dt = 0; dt < kCkvDim / 16; ++dt) {
-            const int d = dt * 16;
-            const uint32_t x0 = v0[d] | (static_cast<uint32_t>(v0[kKStride + d]) << 16);
-            const uint32_t x1 = v0[2 * kKStride + d] | (static_cast<uint32_t>(v0[3 * kKStride + d]) << 16);
-            const uint32_t x2 = v1[d] | (static_cast<uint32_t>(v1[kKStride + d]) << 16);
-            const uint32_t x3 = v1[2 * kKStride + d] | (static_cast<uint32_t>(v1[3 * kKStride + d]) << 16);
-            const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(x0, x1, x2, x3));
-            f32x4_t acc = oacc[dt];
-            if (rescale) {
-              acc[0] *= alpha;
-              acc[1] *= alpha;
-              acc[2] *= alpha;
-              acc[3] *= alpha;
-            }
-            acc = T::mfma16(af, pb_hi, acc);
-            oacc[dt] = T::mfma16(af, pb_lo, acc);
+            const uint2 lo = lds_read_tr16(v0 + dt * 16);
+            const uint2 hi = lds_read_tr16(v1 + dt * 16);
+            const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            oacc[dt] = T::mfma16(af, pb_lo, T::mfma16(af, pb_hi, oacc[dt]));
             if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
           }
         }
+        // The numerators live in accumulation registers across tiles (the
+        // rare rescale above copies them out and back).
+#pragma unroll
+        for (int dt = 0; dt < kCkvDim / 16; ++dt) asm volatile("" : "+a"(oacc[dt]));
       }
       __syncthreads();  // every wave is done with ks before the next store
     }
@@ -456,7 +467,6 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
   const int splits = choose_splits(rows, hgroups);
   SfaArgs args = a;
-  // Fused: ~30% of a row's splits handle the host-sourced miss tiles.
   const Partials p = carve(a.workspace, rows, splits, a.heads);
   launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED>,
                 dim3(static_cast<uint32_t>(rows * splits), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads),
