@@ -38,7 +38,15 @@ HIP kernels implement:
   paired in ascending order with the misses (MTP0: ascending token id;
   MTP3: ordered-union order);
 * an attention key whose slot is negative, >= the visible length, or does
-  not resolve through the block table is left out of the softmax.
+  not resolve through the block table is left out of the softmax;
+* first-decode init gives slot i to the i-th smallest selected token.
+
+Parity unpinned (no reference test or vector fixes them): the reference's own
+victim choice and in-row order where they differ from the rules above, and
+the slot order of ``initialize_lidu_row`` (the reference takes
+``torch.topk(..., sorted=False)``, whose order is implementation-defined).
+Every other output of these functions is pinned by tests/test_oracle.py,
+tests/test_lidu_init.py and tests/test_golden.py.
 
 Scores are computed in float64; the attention golden in float64 (and
 optionally float32 like the reference test).  16-bit tensors are passed as
