@@ -46,7 +46,9 @@ constexpr int kManageThreads = 512;
 constexpr int kDigitBits = 13;                    // radix digit width
 constexpr int kBins = 1 << kDigitBits;            // radix histogram bins
 constexpr int kBinsPerThread = kBins / kManageThreads;
+constexpr int kGatherKeys = 64;                   // radix select: bins this small are ranked directly
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
+constexpr int kTableStride = kSlotStride + kManageThreads;  // workspace slot tables: + one junk word per thread
 constexpr int kLdsSlots = 4096;     // MTP0: cache budgets up to this keep their slot tables in LDS
 constexpr int kLdsSlotsMtp = 8192;  // MTP3 (its LDS holds no register-resident candidates)
 constexpr uint32_t kStateShift = 24;
@@ -72,9 +74,9 @@ LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
   w.scores = reinterpret_cast<float*>(p);
   p += align256(sizeof(float) * batch * queries * cap);
   w.slot_table = reinterpret_cast<uint32_t*>(p);
-  p += align256(sizeof(uint32_t) * batch * kSlotStride);
+  p += align256(sizeof(uint32_t) * batch * kTableStride);
   w.slot_key = reinterpret_cast<uint32_t*>(p);
-  p += align256(sizeof(uint32_t) * batch * kSlotStride);
+  p += align256(sizeof(uint32_t) * batch * kTableStride);
   w.miss_list = reinterpret_cast<int32_t*>(p);
   p += align256(sizeof(int32_t) * batch * kUnionCap);
   w.select = reinterpret_cast<uint32_t*>(p);
@@ -304,6 +306,38 @@ __device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Vis
     remaining -= __builtin_amdgcn_readfirstlane(bcast[1]);
     cnt_eq = __builtin_amdgcn_readfirstlane(bcast[2]);
     __syncthreads();
+    if (lo > 0 && cnt_eq <= kGatherKeys) {
+      // Few keys left in the selected bin: gather them and rank them in one
+      // wave instead of running the remaining digit passes.
+      if (tid == 0) bcast[3] = 0;
+      __syncthreads();
+      visit([&](uint32_t key) {
+        const uint32_t d = key - kmin;
+        if ((d & pmask) == prefix) hist[atomicAdd(&bcast[3], 1)] = d;  // cnt_eq <= kGatherKeys entries
+      });
+      __syncthreads();
+      if (tid < kWave) {
+        const uint32_t mine = tid < cnt_eq ? hist[tid] : 0u;
+        int greater = 0, equal = 0;
+        for (int j = 0; j < cnt_eq; ++j) {
+          const uint32_t o = hist[j];
+          greater += o > mine ? 1 : 0;
+          equal += o == mine ? 1 : 0;
+        }
+        if (tid < cnt_eq && greater < remaining && remaining <= greater + equal) {  // lanes holding the answer
+          bcast[0] = static_cast<int>(mine);
+          bcast[1] = remaining - greater;
+          bcast[2] = equal;
+        }
+      }
+      __syncthreads();
+      const uint32_t x = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bcast[0]));
+      remaining = __builtin_amdgcn_readfirstlane(bcast[1]);
+      cnt_eq = __builtin_amdgcn_readfirstlane(bcast[2]);
+      if (tid < kGatherKeys) hist[tid] = 0u;  // zero again for the next call
+      __syncthreads();
+      return SelectOut{x + kmin, remaining, cnt_eq};
+    }
   }
   return SelectOut{prefix + kmin, remaining, cnt_eq};
 }
@@ -761,9 +795,9 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
   __shared__ int vslot[kTopK];
-  __shared__ int lds_miss[kTopK];
-  __shared__ uint32_t lds_stab[kLdsSlots];
-  __shared__ uint32_t lds_skey[kLdsSlots];
+  __shared__ int lds_miss[kTopK + kManageThreads];       // + one junk word per thread
+  __shared__ uint32_t lds_stab[kLdsSlots + kManageThreads];
+  __shared__ uint32_t lds_skey[kLdsSlots + kManageThreads];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int n = a.num_candidates[b];
@@ -778,8 +812,8 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
   // Slot tables: LDS for budgets up to kLdsSlots, else the workspace.
   const bool lds_tables = c <= kLdsSlots;
-  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kSlotStride;
-  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kSlotStride;
+  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kTableStride;
   int32_t* misses = lds_miss;
 
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
@@ -860,14 +894,18 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
     uint32_t selm[RES], eqm[RES], cachm[RES];
 #pragma unroll
     for (int ch = 0; ch < RES; ++ch) {
-      selm[ch] = eqm[ch] = cachm[ch] = 0u;
+      const int nvalid = n - (ch * kChunk + tid * kItems);  // items e < nvalid are candidates
+      const uint32_t vmask = nvalid >= kItems ? 0xffu : (nvalid <= 0 ? 0u : (1u << nvalid) - 1u);
+      uint32_t sm = 0u, em = 0u, cm = 0u;
 #pragma unroll
       for (int e = 0; e < kItems; ++e) {
-        if (ch * kChunk + tid * kItems + e >= n) continue;
-        if (u[ch][e] > sel.thresh) selm[ch] |= 1u << e;
-        if (u[ch][e] == sel.thresh) eqm[ch] |= 1u << e;
-        if (((pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu) != 0xffffu) cachm[ch] |= 1u << e;
+        sm |= (u[ch][e] > sel.thresh ? 1u : 0u) << e;
+        em |= (u[ch][e] == sel.thresh ? 1u : 0u) << e;
+        cm |= (((pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu) != 0xffffu ? 1u : 0u) << e;
       }
+      selm[ch] = sm & vmask;
+      eqm[ch] = em & vmask;
+      cachm[ch] = cm & vmask;
     }
     if (need_rank) {  // ties at the threshold: the lowest tokens first
       uint64_t cnt[2] = {0, 0}, tot[2];
@@ -895,26 +933,36 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
     for (int ch = 0; ch < RES; ++ch)
       cnt[ch >> 2] |= static_cast<uint64_t>(__popc(selm[ch] & ~cachm[ch])) << (16 * (ch & 3));
     block_exclusive_scan8(cnt, scratch64, tot);
+    // Every item stores unconditionally: entries it does not own go to this
+    // thread's junk word past the slot table (no divergent branch per item;
+    // about 1 item in 15 is cached or missed).  Two instantiations keep the
+    // LDS tables on ds_write (a pointer that may be either is a flat store).
+    auto write_items = [&](uint32_t* tab, uint32_t* key, uint32_t junk) {
+      int tb = tid;
+      asm volatile("" : "+v"(tb));  // token ids are formed here, not hoisted into the radix passes
 #pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {
-      int pos = miss_run + lane16x8(cnt, ch);
-      const int t0 = ch * kChunk + tid * kItems;
-      const uint32_t missm = selm[ch] & ~cachm[ch];
+      for (int ch = 0; ch < RES; ++ch) {
+        int pos = miss_run + lane16x8(cnt, ch);
+        const int t0 = ch * kChunk + tb * kItems;
+        const uint32_t missm = selm[ch] & ~cachm[ch];
 #pragma unroll
-      for (int e = 0; e < kItems; ++e) {
-        if ((missm >> e) & 1u) misses[pos++] = t0 + e;
-        if ((cachm[ch] >> e) & 1u) {
+        for (int e = 0; e < kItems; ++e) {
+          const bool miss = (missm >> e) & 1u;
+          lds_miss[miss ? pos : kTopK + tid] = t0 + e;
+          pos += miss ? 1 : 0;
+          const bool cached = (cachm[ch] >> e) & 1u;
+          const bool hit = (selm[ch] >> e) & 1u;
           const uint32_t slot = (pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu;
-          if ((selm[ch] >> e) & 1u) {
-            stab[slot] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
-          } else {
-            stab[slot] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
-            skey[slot] = u[ch][e] + lo;  // absolute key (free slots rank below every score)
-          }
+          tab[cached ? slot : junk] = static_cast<uint32_t>(t0 + e) | ((hit ? kStateHit : kStateCand) << kStateShift);
+          key[cached && !hit ? slot : junk] = u[ch][e] + lo;  // absolute key (free slots rank below every score)
         }
+        miss_run += lane16x8(tot, ch);
       }
-      miss_run += lane16x8(tot, ch);
-    }
+    };
+    if (lds_tables)
+      write_items(lds_stab, lds_skey, kLdsSlots + tid);
+    else
+      write_items(stab, skey, kSlotStride + tid);
   } else {
     const SelectOut sel = read_select(w, b);  // lim_threshold_kernel
     const bool need_rank = sel.cnt_eq != sel.need_eq;
@@ -958,8 +1006,8 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
   const float* s = w.scores + static_cast<int64_t>(b) * kMtpQueries * cap;
   int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
   const bool lds_tables = c <= kLdsSlotsMtp;
-  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kSlotStride;
-  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kSlotStride;
+  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kTableStride;
   uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
   int32_t* miss_src = a.miss_src + static_cast<int64_t>(b) * kUnionCap;
   int32_t* miss_dst = a.miss_dst + static_cast<int64_t>(b) * kUnionCap;
@@ -1359,7 +1407,7 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
 
 size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries) {
   size_t total = align256(sizeof(float) * batch * queries * source_capacity);
-  total += 2 * align256(sizeof(uint32_t) * batch * kSlotStride);
+  total += 2 * align256(sizeof(uint32_t) * batch * kTableStride);
   total += align256(sizeof(int32_t) * batch * kUnionCap);
   total += align256(sizeof(uint32_t) * 4 * batch * queries);
   if (queries > 1) total += align256(static_cast<size_t>(batch) * source_capacity);
