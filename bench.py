@@ -70,7 +70,8 @@ def parse_args():
 
 
 # ---- hardware-counter helpers ------------------------------------------------
-PMC_KERNELS = ("lim_score_kernel", "lim_manage_mtp_kernel", "lim_manage_kernel", "sfa_split_kernel",
+PMC_KERNELS = ("lim_score_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
+               "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel",
                "sfa_combine_kernel", "scatter_copy_kernel")
 PMC_PROFILE = REPO / "profiles" / "lim_score_cfg1_pmc.txt"
 
@@ -461,8 +462,8 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
         torch.cuda.synchronize()
     step_us = float(np.mean([a.elapsed_time(b) for a, b in times])) * 1000
     misses = int(t["miss_counts"].sum())
-    names = ("lim_score_kernel", "lim_threshold_kernel", "lim_manage_mtp_kernel", "scatter_copy_kernel",
-             "sfa_split_kernel", "sfa_combine_kernel")
+    names = ("lim_score_kernel", "lim_threshold_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel",
+             "lim_mtp_pass_b_kernel", "scatter_copy_kernel", "sfa_split_kernel", "sfa_combine_kernel")
     km = _kernel_means(kt, names)
     n_tokens = int(t["num_candidate_tokens"].sum())
     score_bytes = n_tokens * KEY_ROW_BYTES + 4 * n_tokens * 4

@@ -50,7 +50,6 @@ constexpr int kGatherKeys = 64;                   // radix select: bins this sma
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr int kTableStride = kSlotStride + kManageThreads;  // workspace slot tables: + one junk word per thread
 constexpr int kLdsSlots = 4096;     // MTP0: cache budgets up to this keep their slot tables in LDS
-constexpr int kLdsSlotsMtp = 8192;  // MTP3 (its LDS holds no register-resident candidates)
 constexpr uint32_t kStateShift = 24;
 constexpr uint32_t kStateFree = 0;
 constexpr uint32_t kStateHit = 1;
@@ -64,9 +63,15 @@ struct LimWs {
   uint32_t* slot_table; // [B, 16384] token | state << 24
   uint32_t* slot_key;   // [B, 16384] score key of candidate slots
   int32_t* miss_list;   // [B, 8192]
-  uint32_t* select;     // [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq (threshold kernel)
+  uint32_t* select;     // [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq, tie cutoff token (threshold kernel)
   uint8_t* masks;       // [B, S_cap] per-token query mask (MTP)
+  int32_t* part_counts; // [B, parts, 8] MTP: per chunk, misses by first-selecting query, selected per query
+  int32_t* vslot;       // [B, 8192] MTP: victim slots
+  int32_t* nvict;       // [B] MTP: victims found
 };
+
+// MTP3 management runs one workgroup per kChunk-token chunk of a request.
+__host__ __device__ inline int64_t mtp_parts(int64_t cap) { return (cap + 4095) / 4096; }
 
 LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
   char* p = static_cast<char*>(base);
@@ -81,7 +86,17 @@ LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
   p += align256(sizeof(int32_t) * batch * kUnionCap);
   w.select = reinterpret_cast<uint32_t*>(p);
   p += align256(sizeof(uint32_t) * 4 * batch * queries);
-  w.masks = queries > 1 ? reinterpret_cast<uint8_t*>(p) : nullptr;
+  w.masks = nullptr;
+  w.part_counts = w.vslot = w.nvict = nullptr;
+  if (queries > 1) {
+    w.masks = reinterpret_cast<uint8_t*>(p);
+    p += align256(static_cast<size_t>(batch) * cap);
+    w.part_counts = reinterpret_cast<int32_t*>(p);
+    p += align256(sizeof(int32_t) * batch * mtp_parts(cap) * 8);
+    w.vslot = reinterpret_cast<int32_t*>(p);
+    p += align256(sizeof(int32_t) * batch * kUnionCap);
+    w.nvict = reinterpret_cast<int32_t*>(p);
+  }
   return w;
 }
 
@@ -210,6 +225,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
 
 constexpr int kItems = 8;                          // consecutive tokens per thread in ordered passes
 constexpr int kChunk = kManageThreads * kItems;    // tokens per ordered chunk
+static_assert(kChunk == 4096, "mtp_parts() assumes 4096-token chunks");
 constexpr int kSlotItems = 4;                      // consecutive slots per thread in slot passes
 constexpr int kSlotChunk = kManageThreads * kSlotItems;
 
@@ -574,6 +590,22 @@ __device__ __forceinline__ int select_victims(int c, int m, const uint32_t* stab
   return run < m ? run : m;
 }
 
+// One ordered step of the tie-cutoff search: this thread's tokens
+// [t0, t0 + 32) with key == thresh are the set bits of eqm (bit e = token
+// t0 + e); `before` ties precede this step.  The thread holding the tie of
+// rank `want` (0-based, ascending token) writes its token to bcast[3].
+// Returns the ties seen through this step.  Contains block barriers.
+__device__ inline int tie_cutoff_step(unsigned eqm, int t0, int want, int before, int* scratch, int* bcast) {
+  int tot;
+  const int rk = before + block_exclusive_scan(__popc(eqm), scratch, &tot);
+  if (rk <= want && want < rk + __popc(eqm)) {
+    unsigned m = eqm;
+    for (int k = rk; k < want; ++k) m &= m - 1u;
+    bcast[3] = t0 + __builtin_ctz(m);
+  }
+  return before + tot;
+}
+
 // ---------------------------------------------------------------------------
 // Top-2048 threshold of one (request, query) score row, written to the
 // workspace for a management kernel (MTP3, and MTP0 sources longer than the
@@ -599,6 +631,9 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
   const float* s = w.scores + (static_cast<int64_t>(b) * queries + q) * cap;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   SelectOut sel;
+  // Ties at the threshold go to the lowest tokens: a token with key ==
+  // thresh is selected iff token <= cutoff (INT_MAX when all ties are taken).
+  int cutoff = INT_MAX;
   if constexpr (RES > 0) {
     uint32_t u[RES][kItems];
 #pragma unroll
@@ -651,11 +686,36 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
         ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); },
         hist, scratch, bcast);
   }
+  if (sel.need_eq != sel.cnt_eq) {  // ties at the threshold (rare): one ordered pass finds the last selected
+    const int ngroups = static_cast<int>(ceil_div(n, 4));
+    int before = 0;
+    for (int g0 = 0; g0 < ngroups; g0 += kManageThreads) {
+      const int g = g0 + tid;
+      unsigned eqm = 0u;
+      if (g < ngroups) {
+        uint32_t key[4];
+        bool inc[4];
+        load_score_keys(s, n, 4 * g, key, inc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (inc[e] && key[e] == sel.thresh) eqm |= 1u << e;
+      }
+      before = tie_cutoff_step(eqm, 4 * g, sel.need_eq - 1, before, scratch, bcast);
+    }
+    __syncthreads();
+    cutoff = bcast[3];
+  }
   if (tid == 0) {
     uint32_t* out = w.select + (static_cast<int64_t>(b) * queries + q) * 4;
     out[0] = sel.thresh;
     out[1] = static_cast<uint32_t>(sel.need_eq);
     out[2] = static_cast<uint32_t>(sel.cnt_eq);
+    out[3] = static_cast<uint32_t>(cutoff);
+  }
+  // MTP3: the request's slot table starts all-free for the chunked passes.
+  if (queries > 1 && q == 0) {
+    uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+    for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   }
 }
 
@@ -980,19 +1040,120 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
 }
 
 // ---------------------------------------------------------------------------
-// 2b. MTP3 management: union of the four top-2048 sets.
-__global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs a, LimWs w) {
+// 2b. MTP3 management: union of the four top-2048 sets, in three chunked
+// kernels (one workgroup per 4096-token chunk of a request for the passes):
+//   pass A   query masks, slot states, per-chunk counts;
+//   victims  one workgroup per request: victim radix select over the slots;
+//   pass B   union-ordered misses, per-query rows, pool update, each chunk
+//            placing its entries after the counts of the chunks before it.
+// The threshold kernel has run first: per-query threshold keys with tie
+// cutoffs (so a token's selection needs no ordered tie count) and the
+// request's slot table reset to free.
+
+struct MtpSelect {
+  uint32_t thr[kMtpQueries];
+  int cutoff[kMtpQueries];
+};
+
+__device__ inline MtpSelect read_mtp_select(const LimWs& w, int b) {
+  MtpSelect m;
+#pragma unroll
+  for (int q = 0; q < kMtpQueries; ++q) {
+    const uint32_t* sp = w.select + (static_cast<int64_t>(b) * kMtpQueries + q) * 4;
+    m.thr[q] = sp[0];
+    m.cutoff[q] = static_cast<int>(sp[3]);
+  }
+  return m;
+}
+
+__global__ __launch_bounds__(kManageThreads) void lim_mtp_pass_a_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)) return;
+  const int64_t cap = a.source_capacity;
+  int32_t* counts = w.part_counts + (static_cast<int64_t>(b) * parts + part) * 8;
+  const int t0 = part * kChunk + tid * kItems;
+  if (part * kChunk >= n) {  // a chunk past the candidates adds nothing
+    if (tid < 8) counts[tid] = 0;
+    return;
+  }
+  const MtpSelect ms = read_mtp_select(w, b);
+  const float* s = w.scores + static_cast<int64_t>(b) * kMtpQueries * cap;
+  const int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
+  uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
+
+  uint32_t u[kMtpQueries][kItems];
+  int32_t slot[kItems];
+  bool in[kItems];
+  load_tokens8(s, pool, n, t0, u[0], slot, in);
+#pragma unroll
+  for (int q = 1; q < kMtpQueries; ++q) {
+    const float* sq = s + q * cap;
+    if (t0 + kItems <= n) {
+      const float4 x = *reinterpret_cast<const float4*>(sq + t0);
+      const float4 y = *reinterpret_cast<const float4*>(sq + t0 + 4);
+      u[q][0] = score_key(x.x); u[q][1] = score_key(x.y); u[q][2] = score_key(x.z); u[q][3] = score_key(x.w);
+      u[q][4] = score_key(y.x); u[q][5] = score_key(y.y); u[q][6] = score_key(y.z); u[q][7] = score_key(y.w);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) u[q][e] = in[e] ? score_key(sq[t0 + e]) : 0u;
+    }
+  }
+  unsigned qmask[kItems];
+  uint64_t missp = 0, rowp = 0;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    qmask[e] = 0;
+    if (!in[e]) continue;
+    const int t = t0 + e;
+#pragma unroll
+    for (int q = 0; q < kMtpQueries; ++q)
+      if (u[q][e] > ms.thr[q] || (u[q][e] == ms.thr[q] && t <= ms.cutoff[q])) qmask[e] |= 1u << q;
+    const bool cached = slot[e] >= 0 && slot[e] < c;
+    if (cached) {
+      if (qmask[e]) {
+        stab[slot[e]] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
+      } else {
+        uint32_t umax = u[0][e];
+#pragma unroll
+        for (int q = 1; q < kMtpQueries; ++q) umax = u[q][e] > umax ? u[q][e] : umax;
+        stab[slot[e]] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
+        skey[slot[e]] = umax;
+      }
+    } else if (qmask[e]) {
+      missp += uint64_t{1} << (16 * __builtin_ctz(qmask[e]));
+    }
+#pragma unroll
+    for (int q = 0; q < kMtpQueries; ++q)
+      if ((qmask[e] >> q) & 1u) rowp += uint64_t{1} << (16 * q);
+  }
+  if (t0 + kItems <= n) {
+    const uint32_t m0 = qmask[0] | (qmask[1] << 8) | (qmask[2] << 16) | (qmask[3] << 24);
+    const uint32_t m1 = qmask[4] | (qmask[5] << 8) | (qmask[6] << 16) | (qmask[7] << 24);
+    *reinterpret_cast<uint2*>(masks + t0) = make_uint2(m0, m1);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kItems; ++e)
+      if (in[e]) masks[t0 + e] = static_cast<uint8_t>(qmask[e]);
+  }
+  uint64_t mtot, rtot;
+  (void)block_exclusive_scan4(missp, scratch64, &mtot);
+  (void)block_exclusive_scan4(rowp, scratch64, &rtot);
+  if (tid < 8) counts[tid] = tid < 4 ? lane16(mtot, tid) : lane16(rtot, tid - 4);
+}
+
+__global__ __launch_bounds__(kManageThreads) void lim_mtp_victims_kernel(LimArgs a, LimWs w, int parts) {
   __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
-  __shared__ int vslot[kUnionCap];
-  __shared__ uint32_t lds_stab[kLdsSlotsMtp];
-  __shared__ uint32_t lds_skey[kLdsSlotsMtp];
-  __shared__ uint32_t thr[kMtpQueries];
-  __shared__ int need[kMtpQueries];
-  __shared__ int rank_needed[kMtpQueries];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int n = a.num_candidates[b];
@@ -1002,213 +1163,140 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_mtp_kernel(LimArgs 
     if (tid == 0) a.miss_counts[b] = 0;
     return;
   }
-  const int64_t cap = a.source_capacity;
-  const float* s = w.scores + static_cast<int64_t>(b) * kMtpQueries * cap;
-  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  const bool lds_tables = c <= kLdsSlotsMtp;
-  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kTableStride;
-  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kTableStride;
-  uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
-  int32_t* miss_src = a.miss_src + static_cast<int64_t>(b) * kUnionCap;
-  int32_t* miss_dst = a.miss_dst + static_cast<int64_t>(b) * kUnionCap;
-  const int ngroups = static_cast<int>(ceil_div(n, 4));
-
-  for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  if (tid < kMtpQueries) {  // per-query thresholds from lim_threshold_kernel (one lane each)
-    const uint32_t* sp = w.select + (static_cast<int64_t>(b) * kMtpQueries + tid) * 4;
-    thr[tid] = sp[0];
-    need[tid] = static_cast<int>(sp[1]);
-    rank_needed[tid] = sp[2] != sp[1];
+  const int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
+  int local = 0;
+  for (int p = tid; p < parts; p += kManageThreads)
+    local += counts[p * 8 + 0] + counts[p * 8 + 1] + counts[p * 8 + 2] + counts[p * 8 + 3];
+  const int m = block_sum(local, scratch);  // union misses
+  const int nv = select_victims(c, m, w.slot_table + static_cast<int64_t>(b) * kTableStride,
+                                w.slot_key + static_cast<int64_t>(b) * kTableStride,
+                                w.vslot + static_cast<int64_t>(b) * kUnionCap, hist, scratch, bcast, red);
+  if (tid == 0) {
+    w.nvict[b] = nv;
+    a.miss_counts[b] = m;
   }
-  __syncthreads();
-  const bool any_rank = rank_needed[0] | rank_needed[1] | rank_needed[2] | rank_needed[3];
+}
 
-  // Pass A: query masks, slot states, union misses per first-selecting query.
-  int eq_run[kMtpQueries] = {0, 0, 0, 0};
-  int gmiss[kMtpQueries] = {0, 0, 0, 0};
-  for (int base = 0; base < n; base += kChunk) {
-    const int t0 = base + tid * kItems;
-    uint32_t u[kMtpQueries][kItems];
-    int32_t slot[kItems];
-    bool in[kItems];
-    load_tokens8(s, pool, n, t0, u[0], slot, in);
+__global__ __launch_bounds__(kManageThreads) void lim_mtp_pass_b_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
+  __shared__ uint64_t base[2];
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)) return;
+  if (part * kChunk >= n) return;
+  const int64_t cap = a.source_capacity;
+  // Counts of the chunks before this one (exclusive scan over parts, parts <= 512).
+  const int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
+  uint64_t pm = 0, pr = 0;
+  if (tid < parts) {
 #pragma unroll
-    for (int q = 1; q < kMtpQueries; ++q) {
-      const float* sq = s + q * cap;
-      if (t0 + kItems <= n) {
-        const float4 x = *reinterpret_cast<const float4*>(sq + t0);
-        const float4 y = *reinterpret_cast<const float4*>(sq + t0 + 4);
-        u[q][0] = score_key(x.x); u[q][1] = score_key(x.y); u[q][2] = score_key(x.z); u[q][3] = score_key(x.w);
-        u[q][4] = score_key(y.x); u[q][5] = score_key(y.y); u[q][6] = score_key(y.z); u[q][7] = score_key(y.w);
-      } else {
-#pragma unroll
-        for (int e = 0; e < kItems; ++e) u[q][e] = in[e] ? score_key(sq[t0 + e]) : 0u;
-      }
+    for (int q = 0; q < kMtpQueries; ++q) {
+      pm |= static_cast<uint64_t>(counts[tid * 8 + q]) << (16 * q);
+      pr |= static_cast<uint64_t>(counts[tid * 8 + 4 + q]) << (16 * q);
     }
-    unsigned qmask[kItems];
-    uint64_t eqp = 0;
-    unsigned eqbits[kMtpQueries] = {0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      qmask[e] = 0;
-      if (!in[e]) continue;
-#pragma unroll
-      for (int q = 0; q < kMtpQueries; ++q) {
-        if (u[q][e] > thr[q]) qmask[e] |= 1u << q;
-        if (u[q][e] == thr[q]) {
-          if (rank_needed[q]) {
-            eqbits[q] |= 1u << e;
-            eqp += uint64_t{1} << (16 * q);
-          } else {
-            qmask[e] |= 1u << q;
-          }
-        }
-      }
-    }
-    if (any_rank) {
-      uint64_t tot;
-      const uint64_t rk = block_exclusive_scan4(eqp, scratch64, &tot);
-#pragma unroll
-      for (int q = 0; q < kMtpQueries; ++q) {
-        int rq = eq_run[q] + lane16(rk, q);
-#pragma unroll
-        for (int e = 0; e < kItems; ++e)
-          if ((eqbits[q] >> e) & 1u) {
-            if (rq < need[q]) qmask[e] |= 1u << q;
-            ++rq;
-          }
-        eq_run[q] += lane16(tot, q);
-      }
-    }
-    uint64_t missp = 0;
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      if (!in[e]) continue;
-      const bool cached = slot[e] >= 0 && slot[e] < c;
-      if (cached) {
-        if (qmask[e]) {
-          stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
-        } else {
-          uint32_t umax = u[0][e];
-#pragma unroll
-          for (int q = 1; q < kMtpQueries; ++q) umax = u[q][e] > umax ? u[q][e] : umax;
-          stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
-          skey[slot[e]] = umax;
-        }
-      } else if (qmask[e]) {
-        missp += uint64_t{1} << (16 * __builtin_ctz(qmask[e]));
-      }
-    }
-    if (t0 + kItems <= n) {
-      const uint32_t m0 = qmask[0] | (qmask[1] << 8) | (qmask[2] << 16) | (qmask[3] << 24);
-      const uint32_t m1 = qmask[4] | (qmask[5] << 8) | (qmask[6] << 16) | (qmask[7] << 24);
-      *reinterpret_cast<uint2*>(masks + t0) = make_uint2(m0, m1);
-    } else {
-#pragma unroll
-      for (int e = 0; e < kItems; ++e)
-        if (in[e]) masks[t0 + e] = static_cast<uint8_t>(qmask[e]);
-    }
-    uint64_t tot;
-    (void)block_exclusive_scan4(missp, scratch64, &tot);
-#pragma unroll
-    for (int q = 0; q < kMtpQueries; ++q) gmiss[q] += lane16(tot, q);
+  }
+  uint64_t mall, rall;
+  const uint64_t pm_before = block_exclusive_scan4(pm, scratch64, &mall);
+  const uint64_t pr_before = block_exclusive_scan4(pr, scratch64, &rall);
+  if (tid == part) {
+    base[0] = pm_before;
+    base[1] = pr_before;
   }
   __syncthreads();
-  const int m = gmiss[0] + gmiss[1] + gmiss[2] + gmiss[3];
-  int gbase[kMtpQueries];
+  const uint64_t mb = base[0], rb = base[1];
+  int gbase[kMtpQueries];  // union order: misses first-selected by q0, then q1, ...
   gbase[0] = 0;
 #pragma unroll
-  for (int q = 1; q < kMtpQueries; ++q) gbase[q] = gbase[q - 1] + gmiss[q - 1];
-  const int nv = select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
+  for (int q = 1; q < kMtpQueries; ++q) gbase[q] = gbase[q - 1] + lane16(mall, q - 1);
+  const int nv = w.nvict[b];
+  const int32_t* vslot = w.vslot + static_cast<int64_t>(b) * kUnionCap;
+  const uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  const uint8_t* masks = w.masks + static_cast<int64_t>(b) * cap;
+  int32_t* miss_src = a.miss_src + static_cast<int64_t>(b) * kUnionCap;
+  int32_t* miss_dst = a.miss_dst + static_cast<int64_t>(b) * kUnionCap;
 
-  // Pass B: union-ordered misses, per-query rows, pool update.
-  int gm_run[kMtpQueries] = {0, 0, 0, 0};
-  int row_run[kMtpQueries] = {0, 0, 0, 0};
-  for (int base = 0; base < n; base += kChunk) {
-    const int t0 = base + tid * kItems;
-    unsigned mb[kItems];
-    int32_t slot[kItems];
-    if (t0 + kItems <= n) {
-      const uint2 mm = *reinterpret_cast<const uint2*>(masks + t0);
+  const int t0 = part * kChunk + tid * kItems;
+  unsigned mbits[kItems];
+  int32_t slot[kItems];
+  if (t0 + kItems <= n) {
+    const uint2 mm = *reinterpret_cast<const uint2*>(masks + t0);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        mb[e] = (mm.x >> (8 * e)) & 0xffu;
-        mb[e + 4] = (mm.y >> (8 * e)) & 0xffu;
-      }
-      const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
-      const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
-      slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
-      slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < kItems; ++e) {
-        const bool inb = t0 + e < n;
-        mb[e] = inb ? masks[t0 + e] : 0;
-        slot[e] = inb ? pool[t0 + e] : -1;
-      }
+    for (int e = 0; e < 4; ++e) {
+      mbits[e] = (mm.x >> (8 * e)) & 0xffu;
+      mbits[e + 4] = (mm.y >> (8 * e)) & 0xffu;
     }
-    uint64_t missp = 0, rowp = 0;
+    const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
+    const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
+    slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
+    slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
+  } else {
 #pragma unroll
     for (int e = 0; e < kItems; ++e) {
-      const unsigned mk = mb[e];
-      if (!mk) continue;
-      const bool cached = slot[e] >= 0 && slot[e] < c;
-      if (!cached) missp += uint64_t{1} << (16 * __builtin_ctz(mk));
-#pragma unroll
-      for (int q = 0; q < kMtpQueries; ++q)
-        if ((mk >> q) & 1u) rowp += uint64_t{1} << (16 * q);
-    }
-    uint64_t mtot, rtot;
-    const uint64_t mrk = block_exclusive_scan4(missp, scratch64, &mtot);
-    const uint64_t rrk = block_exclusive_scan4(rowp, scratch64, &rtot);
-    int mpos[kMtpQueries], rpos[kMtpQueries];
-#pragma unroll
-    for (int q = 0; q < kMtpQueries; ++q) {
-      mpos[q] = gbase[q] + gm_run[q] + lane16(mrk, q);
-      rpos[q] = row_run[q] + lane16(rrk, q);
-    }
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      const unsigned mk = mb[e];
-      if (!mk) continue;
-      const int t = t0 + e;
-      const bool cached = slot[e] >= 0 && slot[e] < c;
-      int new_slot = slot[e];
-      if (!cached) {
-        const int g = __builtin_ctz(mk);
-        int pos = 0;
-#pragma unroll
-        for (int q = 0; q < kMtpQueries; ++q)
-          if (q == g) pos = mpos[q]++;
-        const int d = pos < nv ? vslot[pos] : -1;
-        miss_src[pos] = t;
-        miss_dst[pos] = d;
-        new_slot = d;
-        if (d >= 0) {
-          const uint32_t ent = stab[d];
-          if ((ent >> kStateShift) == kStateCand) pool[ent & kTokenMask] = -1;
-          pool[t] = d;
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < kMtpQueries; ++q)
-        if ((mk >> q) & 1u) {
-          const int i = rpos[q]++;
-          const int64_t row = static_cast<int64_t>(b) * kMtpQueries + q;
-          if (i < kTopK) {
-            a.topk_src[row * kTopK + i] = cached ? -1 : t;
-            a.topk_dst[row * kTopK + i] = new_slot;
-          }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < kMtpQueries; ++q) {
-      gm_run[q] += lane16(mtot, q);
-      row_run[q] += lane16(rtot, q);
+      const bool inb = t0 + e < n;
+      mbits[e] = inb ? masks[t0 + e] : 0;
+      slot[e] = inb ? pool[t0 + e] : -1;
     }
   }
-  if (tid == 0) a.miss_counts[b] = m;
+  uint64_t missp = 0, rowp = 0;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    const unsigned mk = mbits[e];
+    if (!mk) continue;
+    const bool cached = slot[e] >= 0 && slot[e] < c;
+    if (!cached) missp += uint64_t{1} << (16 * __builtin_ctz(mk));
+#pragma unroll
+    for (int q = 0; q < kMtpQueries; ++q)
+      if ((mk >> q) & 1u) rowp += uint64_t{1} << (16 * q);
+  }
+  uint64_t mtot, rtot;
+  const uint64_t mrk = block_exclusive_scan4(missp, scratch64, &mtot);
+  const uint64_t rrk = block_exclusive_scan4(rowp, scratch64, &rtot);
+  int mpos[kMtpQueries], rpos[kMtpQueries];
+#pragma unroll
+  for (int q = 0; q < kMtpQueries; ++q) {
+    mpos[q] = gbase[q] + lane16(mb, q) + lane16(mrk, q);
+    rpos[q] = lane16(rb, q) + lane16(rrk, q);
+  }
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    const unsigned mk = mbits[e];
+    if (!mk) continue;
+    const int t = t0 + e;
+    const bool cached = slot[e] >= 0 && slot[e] < c;
+    int new_slot = slot[e];
+    if (!cached) {
+      const int g = __builtin_ctz(mk);
+      int pos = 0;
+#pragma unroll
+      for (int q = 0; q < kMtpQueries; ++q)
+        if (q == g) pos = mpos[q]++;
+      const int d = pos < nv ? vslot[pos] : -1;
+      miss_src[pos] = t;
+      miss_dst[pos] = d;
+      new_slot = d;
+      if (d >= 0) {
+        const uint32_t ent = stab[d];
+        if ((ent >> kStateShift) == kStateCand) pool[ent & kTokenMask] = -1;  // an unselected token: no chunk reads it
+        pool[t] = d;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kMtpQueries; ++q)
+      if ((mk >> q) & 1u) {
+        const int i = rpos[q]++;
+        const int64_t row = static_cast<int64_t>(b) * kMtpQueries + q;
+        if (i < kTopK) {
+          a.topk_src[row * kTopK + i] = cached ? -1 : t;
+          a.topk_dst[row * kTopK + i] = new_slot;
+        }
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1396,7 +1484,12 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (Q > 1) {
-    launch_kernel(kKernLimManageMtp, lim_manage_mtp_kernel, mgrid, mblock, stream, a, w);
+    const int parts = static_cast<int>(mtp_parts(a.source_capacity));
+    if (parts > kManageThreads) return hipErrorInvalidValue;  // pass B scans one part per thread
+    const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
+    launch_kernel(kKernLimMtpPassA, lim_mtp_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
+    launch_kernel(kKernLimMtpVictims, lim_mtp_victims_kernel, mgrid, mblock, stream, a, w, parts);
+    launch_kernel(kKernLimMtpPassB, lim_mtp_pass_b_kernel, pgrid, mblock, stream, a, w, parts);
   } else {
     launch_kernel(kKernLimManage, lim_manage_kernel<0>, mgrid, mblock, stream, a, w);
   }
@@ -1410,7 +1503,12 @@ size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries) 
   total += 2 * align256(sizeof(uint32_t) * batch * kTableStride);
   total += align256(sizeof(int32_t) * batch * kUnionCap);
   total += align256(sizeof(uint32_t) * 4 * batch * queries);
-  if (queries > 1) total += align256(static_cast<size_t>(batch) * source_capacity);
+  if (queries > 1) {
+    total += align256(static_cast<size_t>(batch) * source_capacity);
+    total += align256(sizeof(int32_t) * batch * mtp_parts(source_capacity) * 8);
+    total += align256(sizeof(int32_t) * batch * kUnionCap);
+    total += align256(sizeof(int32_t) * batch);
+  }
   return total;
 }
 

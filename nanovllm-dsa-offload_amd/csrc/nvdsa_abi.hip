@@ -169,9 +169,9 @@ int nvdsa_profile_end(float* durations_ms, int32_t* kernel_ids, int32_t capacity
 
 const char* nvdsa_kernel_name(int32_t kernel_id) {
   static const char* names[] = {"scatter_copy_kernel", "lim_score_kernel",   "lim_manage_kernel",
-                                "lim_manage_mtp_kernel", "sfa_split_kernel", "sfa_split_kernel_fused",
+                                "lim_mtp_pass_a_kernel", "sfa_split_kernel", "sfa_split_kernel_fused",
                                 "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel",
-                                "lim_threshold_kernel"};
+                                "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel"};
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }

@@ -16,14 +16,16 @@ enum KernelId : int {
   kKernScatter = 0,
   kKernLimScore = 1,
   kKernLimManage = 2,
-  kKernLimManageMtp = 3,
+  kKernLimMtpPassA = 3,
   kKernSfaSplit = 4,
   kKernSfaSplitFused = 5,
   kKernSfaCombine = 6,
   kKernLiduInit = 7,
   kKernLiduShared = 8,
   kKernLimThreshold = 9,
-  kKernCount = 10
+  kKernLimMtpVictims = 10,
+  kKernLimMtpPassB = 11,
+  kKernCount = 12
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.

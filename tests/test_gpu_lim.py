@@ -170,6 +170,59 @@ def test_lim_mtp_bit_exact(heads):
     assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
 
 
+def _tie_case(mtp: bool, positives, seed=11):
+    """Scores with exact ties at the top-2048 threshold: query row j of a
+    request reads key dim j only, and key dim j is positive for `positives[j]`
+    tokens of the request (values 1 + m/128, exact in 16 bits), zero
+    otherwise, so after ReLU every other token scores exactly 0 and the
+    2048th score is a 0 shared by thousands of tokens (lowest tokens win)."""
+    from nanovllm_amd.workloads import make_chain_case
+
+    B, N = 3, 12288
+    case = make_chain_case(B, N, [8192, 8704, 10240] if mtp else [2048, 4096, 6144], [4, 20, 60], seed=seed,
+                           mtp=mtp, guard=False)
+    t = case.tensors
+    Q = 4 if mtp else 1
+    q = torch.zeros(B * Q, 32, 128)
+    w = torch.zeros(B * Q, 32)
+    for j in range(Q):
+        q[j::Q, 0, j] = 1.0
+    w[:, 0] = 1.0
+    t["query_index"].copy_(q.to(t["query_index"].dtype))
+    t["index_weights"].copy_(w.to(t["index_weights"].dtype))
+    keys = t["index_key_cache"].view(-1, 128, 128).float()
+    keys.zero_()
+    table = t["index_block_table"]
+    rng = np.random.default_rng(seed)
+    for b in range(B):
+        for j in range(Q):
+            toks = rng.choice(N, size=positives[j], replace=False)
+            vals = 1.0 + (rng.integers(0, 128, size=toks.size) / 128.0)
+            blk = table[b, torch.from_numpy(toks // 128)].long()
+            keys[blk, torch.from_numpy(toks % 128), j] = torch.from_numpy(vals).float()
+    t["index_key_cache"].copy_(keys.view_as(t["index_key_cache"]).to(t["index_key_cache"].dtype))
+    return case
+
+
+@pytest.mark.parametrize("mtp,positives", [(False, [700]), (True, [500, 900, 1300, 1900])])
+def test_lim_ties_at_threshold_bit_exact(mtp, positives):
+    case = _tie_case(mtp, positives)
+    print(f"LIM ties mtp={mtp} positives={positives}", flush=True)
+    expect = oracle_lim(case, mtp=mtp)
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d, mtp=mtp)
+    mc = ints(d["miss_counts"])
+    assert np.array_equal(mc, expect["miss_counts"])
+    assert np.array_equal(ints(d["topk_src_ids"]), expect["src"])
+    assert np.array_equal(ints(d["topk_dst_slots"]), expect["dst"])
+    if mtp:
+        ms, md = ints(d["miss_src_ids"]), ints(d["miss_dst_slots"])
+        for b in range(mc.size):
+            assert np.array_equal(ms[b, :mc[b]], expect["miss_src"][b, :mc[b]])
+            assert np.array_equal(md[b, :mc[b]], expect["miss_dst"][b, :mc[b]])
+    assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
+
+
 def test_lim_row_guards():
     from nanovllm_amd.workloads import make_chain_case
 
