@@ -171,7 +171,8 @@ const char* nvdsa_kernel_name(int32_t kernel_id) {
   static const char* names[] = {"scatter_copy_kernel", "lim_score_kernel",   "lim_manage_kernel",
                                 "lim_mtp_pass_a_kernel", "sfa_split_kernel", "sfa_split_kernel_fused",
                                 "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel",
-                                "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel"};
+                                "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
+                                "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied"};
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }
@@ -813,6 +814,7 @@ int run_fused(const char* op, const AttnTensors& t, int64_t rows_per_request, co
   a.copy_dst = static_cast<const int32_t*>(mtp ? miss_dst->data : t.topk_dst->data);
   a.copy_counts = static_cast<const int32_t*>(miss_counts->data);
   a.copy_cap = mtp ? nvdsa::kUnionCap : nvdsa::kTopK;
+  a.key_src = mtp ? static_cast<const int32_t*>(topk_src->data) : nullptr;
   a.dram_table = static_cast<const int32_t*>(dram_table->data);
   a.dram_kpe = dram_kpe->data;
   a.dram_ckv = dram_ckv->data;

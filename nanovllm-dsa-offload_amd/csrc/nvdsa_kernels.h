@@ -25,7 +25,9 @@ enum KernelId : int {
   kKernLimThreshold = 9,
   kKernLimMtpVictims = 10,
   kKernLimMtpPassB = 11,
-  kKernCount = 12
+  kKernSfaMtpOverlap = 12,
+  kKernSfaSplitCopied = 13,
+  kKernCount = 14
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.
@@ -163,6 +165,7 @@ struct SfaArgs {
   const void* dram_ckv;
   int64_t dram_cols;
   int64_t dram_blocks;
+  const int32_t* key_src;       // MTP3 fused: topk_src_ids [R, 2048] (>= 0: a key copied by this call)
   void* workspace;
   size_t workspace_bytes;
 };

@@ -57,4 +57,54 @@ __device__ inline void store_row(uint4* __restrict__ ckv, uint4* __restrict__ kp
   if (lane < (kKpeDim * 2 / 16)) kpe[row * (kKpeDim * 2 / 16) + lane] = d.kpe;
 }
 
+// A wavefront copies pairs [first, first + 4) of request b (those below
+// `count`): every host load issued before any HBM store, so 4 rows of PCIe
+// reads are in flight per wave.  `A` is ScatterArgs (nvdsa_kernels.h).
+template <typename A>
+__device__ inline void copy_pairs4(const A& a, int64_t b, int64_t first, int64_t count, int lane) {
+  constexpr int kRows = 4;
+  const int32_t* src_ids = a.src_ids + b * a.cap;
+  const int32_t* dst_slots = a.dst_slots + b * a.cap;
+  const int32_t* dram_row_table = a.dram_table + b * a.dram_cols;
+  const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
+  RowAddr addr[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int64_t i = first + j;
+    addr[j] = i < count ? resolve_pair(src_ids[i], dst_slots[i], dram_row_table, a.dram_cols, a.dram_blocks,
+                                       hbm_row_table, a.hbm_cols, a.hbm_blocks)
+                        : RowAddr{-1, -1};
+  }
+  RowData data[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j)
+    if (addr[j].src_row >= 0)
+      data[j] = load_row(static_cast<const uint4*>(a.dram_ckv), static_cast<const uint4*>(a.dram_kpe), addr[j].src_row,
+                         lane);
+#pragma unroll
+  for (int j = 0; j < kRows; ++j)
+    if (addr[j].src_row >= 0)
+      store_row(static_cast<uint4*>(a.hbm_ckv), static_cast<uint4*>(a.hbm_kpe), addr[j].dst_row, lane, data[j]);
+}
+
+// Workgroup `wg` of `nwg` (4 waves) copies the 16-pair chunks g = wg,
+// wg + nwg, ... of the concatenation of every request's copy list (a
+// grid-stride loop over all chunks, so every workgroup has work until the
+// lists run out).
+template <typename A>
+__device__ inline void scatter_copy_wg(const A& a, int wg, int nwg) {
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  int64_t base = 0;  // chunks of the requests before b
+  for (int64_t b = 0; b < a.batch; ++b) {
+    int64_t count = a.copy_counts[b];
+    count = count < 0 ? 0 : (count > a.cap ? a.cap : count);
+    const int64_t chunks = (count + 15) / 16;
+    // first global chunk index >= base that is congruent to wg (mod nwg)
+    const int64_t first = base + ((wg - base) % nwg + nwg) % nwg;
+    for (int64_t g = first; g < base + chunks; g += nwg) copy_pairs4(a, b, (g - base) * 16 + wave * 4, count, lane);
+    base += chunks;
+  }
+}
+
 }  // namespace nvdsa

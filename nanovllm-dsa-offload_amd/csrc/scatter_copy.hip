@@ -32,37 +32,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void scatter_copy_kernel(Sc
   const int64_t first = chunk * kRowsPerBlock + wave * kRowsPerWave;
   if (first >= count) return;
 
-  const int32_t* src_ids = a.src_ids + b * a.cap;
-  const int32_t* dst_slots = a.dst_slots + b * a.cap;
-  const int32_t* dram_row_table = a.dram_table + b * a.dram_cols;
-  const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
-
-  RowAddr addr[kRowsPerWave];
-#pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) {
-    const int64_t i = first + j;
-    if (i < count) {
-      addr[j] = resolve_pair(src_ids[i], dst_slots[i], dram_row_table, a.dram_cols, a.dram_blocks,
-                             hbm_row_table, a.hbm_cols, a.hbm_blocks);
-    } else {
-      addr[j] = RowAddr{-1, -1};
-    }
-  }
-  RowData data[kRowsPerWave];
-#pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) {
-    if (addr[j].src_row >= 0) {
-      data[j] = load_row(static_cast<const uint4*>(a.dram_ckv), static_cast<const uint4*>(a.dram_kpe),
-                         addr[j].src_row, lane);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) {
-    if (addr[j].src_row >= 0) {
-      store_row(static_cast<uint4*>(a.hbm_ckv), static_cast<uint4*>(a.hbm_kpe), addr[j].dst_row, lane,
-                data[j]);
-    }
-  }
+  copy_pairs4(a, b, first, count, lane);
 }
 
 }  // namespace

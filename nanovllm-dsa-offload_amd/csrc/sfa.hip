@@ -32,6 +32,7 @@
 //   run side by side.  fused_copy_sfa_mtp: the union misses are
 //   not tile-aligned to any one query row, so the union is copied first
 //   (scatter_copy) and the MTP attention follows on the same stream.
+#include <algorithm>
 #include <cfloat>
 
 #include "nvdsa_common.h"
@@ -111,10 +112,23 @@ Partials carve(void* ws, int64_t rows, int64_t splits, int64_t heads) {
   return p;
 }
 
+// MTP3 overlap launch: XCDs [0, kCopyXcds) copy (one XCD pulls ~13 GB/s
+// from host memory), the others attend; 32 CUs per XCD, one resident
+// workgroup per CU.
+constexpr int kCopyXcds = 5;
+constexpr int kCopyWgs = kCopyXcds * 32;
+int overlap_splits(int64_t rows, int64_t head_groups) {
+  // About two workgroups per attention CU: the rows' tiles spread evenly.
+  int64_t s = ceil_div(2 * (8 - kCopyXcds) * 32, rows * head_groups);
+  if (s < 1) s = 1;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return static_cast<int>(s);
+}
+
 int choose_splits(int64_t rows, int64_t head_groups) {
   if (rows <= 0 || head_groups <= 0) return 1;
-  // One resident workgroup per CU (the LDS footprint allows one): fill the
-  // 256 CUs in a single round.
+  // One resident workgroup per CU (the register footprint allows one): fill
+  // the 256 CUs in a single round.
   const int64_t target = 256;
   int64_t s = target / (rows * head_groups);
   if (s < 1) s = 1;
@@ -122,18 +136,29 @@ int choose_splits(int64_t rows, int64_t head_groups) {
   return static_cast<int>(s);
 }
 
-template <typename T, bool FUSED>
-__global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Partials part, int splits) {
+// Key selection of a split-attention launch over a row's list:
+enum KeyMode : int {
+  kKeysAll = 0,      // every sparse entry plus the tail
+  kKeysResident = 1, // MTP3 overlap, first launch: sparse entries whose key_src < 0 (HBM-resident) plus the tail
+  kKeysCopied = 2,   // MTP3 overlap, second launch: only sparse entries whose key_src >= 0 (copied misses)
+};
+
+// One split of one row: block index `bid` = row * splits + split; its
+// partials go to split slot split_base + split of splits_total per row.
+template <typename T, bool FUSED, int MODE>
+__device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials& part, int splits, int split_base,
+                                               int splits_total, int64_t bid, int hg) {
   __shared__ uint16_t ks[kTileKeys * kKStride];       // key tile, row-major
+  __shared__ int16_t cpos[MODE == kKeysCopied ? kTopK : 1];  // kKeysCopied: list positions of the copied keys
+  __shared__ int scan_scratch[kAttnThreads / 64 + 1];
   // Resolved keys of the current window of kWindowTiles tiles (one per thread):
   // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to, flags.
   __shared__ int64_t win_src[kWindowKeys];
   __shared__ int64_t win_dst[kWindowKeys];
   __shared__ int win_flag[kWindowKeys];  // bit 0: attend, bit 1: source is DRAM, bit 2: source valid
 
-  const int64_t row = blockIdx.x / splits;
-  const int split = static_cast<int>(blockIdx.x - row * splits);
-  const int hg = blockIdx.y;
+  const int64_t row = bid / splits;
+  const int split = static_cast<int>(bid - row * splits);
   const int64_t b = row / a.rows_per_request;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -145,7 +170,29 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   const int head = h0 + l16;
   const int64_t H = a.heads;
 
-  const RowPlan plan = plan_row(a, row);
+  RowPlan plan = plan_row(a, row);
+  if (MODE == kKeysCopied) {
+    // Compact the positions j < 2048 with key_src >= 0 (8 per thread, in
+    // order); the launch attends those entries only, and no tail.
+    int n_copied = 0;
+    if (plan.active && plan.sparse > 0) {
+      const int32_t* ksrc = a.key_src + row * kTopK;
+      constexpr int kPer = kTopK / kAttnThreads;
+      unsigned bits = 0u;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e)
+        if (ksrc[tid * kPer + e] >= 0) bits |= 1u << e;
+      int tot;
+      int pos = block_exclusive_scan(__popc(bits), scan_scratch, &tot);
+#pragma unroll
+      for (int e = 0; e < kPer; ++e)
+        if ((bits >> e) & 1u) cpos[pos++] = static_cast<int16_t>(tid * kPer + e);
+      n_copied = tot;
+      __syncthreads();
+    }
+    plan.sparse = n_copied;
+    plan.count = n_copied;
+  }
   // Copy work (fused): MTP0 copies pairs j < miss_counts[b] of the row's own list.
   int copy_count = 0;
   if (FUSED) {
@@ -154,7 +201,7 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   }
   const int list_len = plan.active ? plan.count : (FUSED ? copy_count : 0);
   const int ntiles = static_cast<int>(ceil_div(list_len, kTileKeys));
-  const int64_t pidx = (row * splits + split) * H + head;
+  const int64_t pidx = (row * splits_total + split_base + split) * H + head;
   // Tiles of this split: t_first, t_first + t_stride, ... < t_end.  Fused:
   // splits [0, miss_splits) take the tiles holding host-sourced misses (the
   // first ceil(copy_count/32) tiles), the others the HBM-only tiles, so the
@@ -219,14 +266,16 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
     int64_t src = -1, dst = -1;
     int flag = 0;
     if (idx < my_tiles && j < list_len) {
-      const int slot = plan.active ? (j < plan.sparse ? topk[j] : plan.tail_start + (j - plan.sparse))
+      const int lj = MODE == kKeysCopied ? cpos[j] : j;  // position in the row's list
+      const int slot = plan.active ? (j < plan.sparse ? topk[lj] : plan.tail_start + (j - plan.sparse))
                                    : a.copy_dst[b * a.copy_cap + j];
+      const bool skip = MODE == kKeysResident && j < plan.sparse && a.key_src[row * kTopK + j] >= 0;
       int64_t hrow = -1;
       if (slot >= 0 && (slot >> kBlockShift) < a.hbm_cols) {
         const int32_t blk = hbm_row_table[slot >> kBlockShift];
         if (blk >= 0 && blk < a.hbm_blocks) hrow = static_cast<int64_t>(blk) * kBlock + (slot & (kBlock - 1));
       }
-      if (plan.active && hrow >= 0 && slot < plan.lvis) {
+      if (plan.active && hrow >= 0 && slot < plan.lvis && !skip) {
         flag = 1 | 4;
         src = hrow;
       }
@@ -424,6 +473,37 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
   }
 }
 
+template <typename T, bool FUSED, int MODE>
+__global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Partials part, int splits, int split_base,
+                                                                 int splits_total) {
+  sfa_split_body<T, FUSED, MODE>(a, part, splits, split_base, splits_total, blockIdx.x, blockIdx.y);
+}
+
+// MTP3 fused_copy_sfa, first launch: attention over the HBM-resident keys
+// (kKeysResident) and the DRAM -> HBM copy of the union misses, side by side
+// on separate XCDs.  Workgroups are dealt to the 8 XCDs round-robin by
+// linear id; those on XCDs [0, kCopyXcds) copy (a grid-stride loop over
+// 16-row chunks of every request), the rest attend.  Host reads in flight
+// stall HBM reads issued on the same XCD, so the two roles do not share one.
+// No workgroup waits on another: the copied keys are attended by a second
+// launch on the same stream.
+template <typename T>
+__global__ __launch_bounds__(kAttnThreads) void sfa_mtp_overlap_kernel(SfaArgs a, Partials part, int splits,
+                                                                       int splits_total, ScatterArgs sc,
+                                                                       int attn_blocks, int hgroups, int copy_wgs) {
+  const int p = blockIdx.x;
+  const int xcd = p & 7;
+  const int slot = p >> 3;
+  if (xcd < kCopyXcds) {
+    const int wg = slot * kCopyXcds + xcd;
+    if (wg < copy_wgs) scatter_copy_wg(sc, wg, copy_wgs);
+    return;
+  }
+  const int i = slot * (8 - kCopyXcds) + (xcd - kCopyXcds);
+  if (i >= attn_blocks * hgroups) return;
+  sfa_split_body<T, false, kKeysResident>(a, part, splits, 0, splits_total, i % attn_blocks, i / attn_blocks);
+}
+
 // Merge split partials: one 128-thread workgroup per (row, head), 4 dims per thread.
 template <typename T>
 __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
@@ -468,9 +548,9 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int splits = choose_splits(rows, hgroups);
   SfaArgs args = a;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
-  launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED>,
+  launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED, kKeysAll>,
                 dim3(static_cast<uint32_t>(rows * splits), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads),
-                stream, args, p, splits);
+                stream, args, p, splits, 0, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>,
@@ -478,11 +558,56 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// MTP3 fused_copy_sfa: the overlap launch (HBM-resident keys + the union
+// copy), then the copied keys, then the merge of both launches' partials.
+template <typename T>
+hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
+  const int64_t rows = a.batch * a.rows_per_request;
+  if (rows == 0) return hipSuccess;
+  const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
+  const int s1 = overlap_splits(rows, hgroups);
+  const int s2 = choose_splits(rows, hgroups);
+  const int total = s1 + s2;
+  const Partials p = carve(a.workspace, rows, total, a.heads);
+  ScatterArgs sc{};
+  sc.src_ids = a.copy_src;
+  sc.dst_slots = a.copy_dst;
+  sc.copy_counts = a.copy_counts;
+  sc.hbm_table = a.hbm_table;
+  sc.dram_table = a.dram_table;
+  sc.hbm_kpe = a.hbm_kpe;
+  sc.hbm_ckv = a.hbm_ckv;
+  sc.dram_kpe = a.dram_kpe;
+  sc.dram_ckv = a.dram_ckv;
+  sc.batch = a.batch;
+  sc.cap = a.copy_cap;
+  sc.hbm_cols = a.hbm_cols;
+  sc.dram_cols = a.dram_cols;
+  sc.hbm_blocks = a.hbm_blocks;
+  sc.dram_blocks = a.dram_blocks;
+  const int attn_blocks = static_cast<int>(rows * s1);
+  const int64_t slots = std::max(ceil_div(kCopyWgs, kCopyXcds), ceil_div(attn_blocks * hgroups, 8 - kCopyXcds));
+  launch_kernel(kKernSfaMtpOverlap, sfa_mtp_overlap_kernel<T>, dim3(static_cast<uint32_t>(8 * slots)),
+                dim3(kAttnThreads), stream, a, p, s1, total, sc, attn_blocks, static_cast<int>(hgroups), kCopyWgs);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  launch_kernel(kKernSfaSplitCopied, sfa_split_kernel<T, false, kKeysCopied>,
+                dim3(static_cast<uint32_t>(rows * s2), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads), stream, a,
+                p, s2, s1, total);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>,
+                dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads)), dim3(128), stream, a, p, total);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens) {
   (void)max_kv_tokens;
-  const int64_t splits = choose_splits(query_rows, ceil_div(heads, kHeadsPerBlock));
+  const int64_t hg = ceil_div(heads, kHeadsPerBlock);
+  const int64_t splits = std::max<int64_t>(choose_splits(query_rows, hg),
+                                          overlap_splits(query_rows, hg) + choose_splits(query_rows, hg));
   return align256(sizeof(float) * query_rows * splits * heads * kCkvDim) +
          align256(sizeof(float) * query_rows * splits * heads * 2);
 }
@@ -492,28 +617,8 @@ hipError_t launch_sparse_tail_attention(const SfaArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream) {
-  if (a.rows_per_request > 1) {
-    // MTP3: copy the compact union misses, then attend; both on `stream`.
-    ScatterArgs s{};
-    s.src_ids = a.copy_src;
-    s.dst_slots = a.copy_dst;
-    s.copy_counts = a.copy_counts;
-    s.hbm_table = a.hbm_table;
-    s.dram_table = a.dram_table;
-    s.hbm_kpe = a.hbm_kpe;
-    s.hbm_ckv = a.hbm_ckv;
-    s.dram_kpe = a.dram_kpe;
-    s.dram_ckv = a.dram_ckv;
-    s.batch = a.batch;
-    s.cap = a.copy_cap;
-    s.hbm_cols = a.hbm_cols;
-    s.dram_cols = a.dram_cols;
-    s.hbm_blocks = a.hbm_blocks;
-    s.dram_blocks = a.dram_blocks;
-    hipError_t e = launch_scatter_copy(s, stream);
-    if (e != hipSuccess) return e;
-    return launch_sparse_tail_attention(a, stream);
-  }
+  if (a.rows_per_request > 1)  // MTP3: the union misses are not tile-aligned to any one query row
+    return a.elem == Elem::kBf16 ? launch_fused_mtp<Bf16>(a, stream) : launch_fused_mtp<F16>(a, stream);
   return a.elem == Elem::kBf16 ? launch_sfa<Bf16, true>(a, stream) : launch_sfa<F16, true>(a, stream);
 }
 
