@@ -462,6 +462,7 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
         torch.cuda.synchronize()
     step_us = float(np.mean([a.elapsed_time(b) for a, b in times])) * 1000
     misses = int(t["miss_counts"].sum())
+    graph_us = _graph_step_us(torch, [step], reps, prepare=lambda: t["cache_slots_pool"].copy_(pool0))
     names = ("lim_score_kernel", "lim_threshold_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel",
              "lim_mtp_pass_b_kernel", "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied", "sfa_combine_kernel")
     km = _kernel_means(kt, names)
@@ -469,7 +470,8 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
     score_bytes = n_tokens * KEY_ROW_BYTES + 4 * n_tokens * 4
     keys = int(sum(2048 + int(L) - int(c) for L, c in zip(t["actual_seq_lengths_kv"].tolist(),
                                                            t["num_cache_tokens"].tolist())))
-    out = {"workload": "bs=16 x 4 queries, prompts 49152, C=8192, tails U[4,127]", "step_us": round(step_us, 2),
+    out = {"workload": "bs=16 x 4 queries, prompts 49152, C=8192, tails U[4,127], HIP-graph replay",
+           "step_us": round(graph_us, 2), "eager_step_us": round(step_us, 2),
            "union_misses_per_step": misses, "kernels_us": km,
            "lim_score_hbm_GBs": round(score_bytes / (km["lim_score_kernel"] * 1e-6) / 1e9, 1),
            # the overlap kernel copies the union misses while attending the HBM-resident keys
@@ -479,6 +481,38 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
     del d, t, case
     torch.cuda.empty_cache()
     return out
+
+
+def _graph_step_us(torch, fns, reps, prepare=None):
+    """Mean µs per replay of HIP graphs captured from ``fns`` (replayed in
+    turn); ``prepare()`` runs before each replay, outside the timed span."""
+    stream = torch.cuda.Stream()
+    graphs = []
+    with torch.cuda.stream(stream):
+        for f in fns:  # warm the capture stream
+            if prepare:
+                prepare()
+            f()
+        stream.synchronize()
+        for f in fns:
+            if prepare:
+                prepare()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                f()
+            graphs.append(g)
+    torch.cuda.synchronize()
+    total_ms = 0.0
+    for i in range(reps):
+        if prepare:
+            prepare()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graphs[i % len(graphs)].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        total_ms += e0.elapsed_time(e1)
+    return total_ms / reps * 1000
 
 
 def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
@@ -527,10 +561,12 @@ def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
     torch.cuda.synchronize()
     km = _kernel_means(kt, ("lim_score_kernel", "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel_fused",
                             "sfa_combine_kernel"))
+    graph_us = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps)  # parity 0: an even number ran
     n_tokens = int(t["num_candidate_tokens"].sum())
     miss_rows = float(np.mean(misses))
-    out = {"workload": "bs=64, prompts U[20K,64K], C=2048, tails U[1,127], misses 5-15%, eager",
-           "step_us": round(step_us, 2), "candidate_tokens": n_tokens, "miss_rows_per_step": round(miss_rows, 1),
+    out = {"workload": "bs=64, prompts U[20K,64K], C=2048, tails U[1,127], misses 5-15%, HIP-graph replay",
+           "step_us": round(graph_us, 2), "eager_step_us": round(step_us, 2), "candidate_tokens": n_tokens,
+           "miss_rows_per_step": round(miss_rows, 1),
            "kernels_us": km,
            "lim_score_hbm_GBs": round((n_tokens * KEY_ROW_BYTES + 4 * n_tokens) / (km["lim_score_kernel"] * 1e-6)
                                       / 1e9, 1),

@@ -606,6 +606,91 @@ __device__ inline int tie_cutoff_step(unsigned eqm, int t0, int want, int before
   return before + tot;
 }
 
+// select_victims with the slot states and keys held in registers: thread t
+// owns slots [t*ITEMS, (t+1)*ITEMS) (slot order = thread-major order), read
+// once.  Same result as select_victims; requires c <= ITEMS * kManageThreads
+// and tables readable up to ITEMS * kManageThreads entries.
+template <int ITEMS>
+__device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot,
+                                                   uint32_t* hist, int* scratch, int* bcast, uint32_t* red) {
+  static_assert(ITEMS % 4 == 0, "vector loads of four slots");
+  const int tid = threadIdx.x;
+  if (m <= 0) return 0;
+  const int i0 = tid * ITEMS;
+  uint32_t key[ITEMS];
+  unsigned nh = 0u;  // non-hit slots (victim candidates) below c
+  {
+    uint32_t st[ITEMS], kv[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS / 4; ++j) {
+      const uint4 a = *reinterpret_cast<const uint4*>(stab + i0 + 4 * j);
+      const uint4 b = *reinterpret_cast<const uint4*>(skey + i0 + 4 * j);
+      st[4 * j] = a.x; st[4 * j + 1] = a.y; st[4 * j + 2] = a.z; st[4 * j + 3] = a.w;
+      kv[4 * j] = b.x; kv[4 * j + 1] = b.y; kv[4 * j + 2] = b.z; kv[4 * j + 3] = b.w;
+    }
+#pragma unroll
+    for (int e = 0; e < ITEMS; ++e) {
+      const uint32_t state = st[e] >> kStateShift;
+      key[e] = ~(state == kStateFree ? 0u : kv[e]);  // smallest score = largest inverted key; free slots first
+      if (i0 + e < c && state != kStateHit) nh |= 1u << e;
+    }
+  }
+  uint32_t lo = 0xffffffffu, hi = 0u;
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e)
+    if ((nh >> e) & 1u) {
+      lo = min(lo, key[e]);
+      hi = max(hi, key[e]);
+    }
+  const int nonhit = block_sum(__popc(nh), scratch);
+  const bool take_all = m >= nonhit;
+  SelectOut sel{0, 0, 0};
+  if (!take_all) {
+    block_minmax(lo, hi, red);
+    sel = radix_select_visit(
+        m, lo, hi,
+        [&](auto&& fn) {
+#pragma unroll
+          for (int e = 0; e < ITEMS; ++e)
+            if ((nh >> e) & 1u) fn(key[e]);
+        },
+        hist, scratch, bcast);
+  }
+  unsigned vmask = 0u, eqmask = 0u;
+  if (take_all) {
+    vmask = nh;
+  } else {
+#pragma unroll
+    for (int e = 0; e < ITEMS; ++e)
+      if ((nh >> e) & 1u) {
+        if (key[e] > sel.thresh) vmask |= 1u << e;
+        if (key[e] == sel.thresh) eqmask |= 1u << e;
+      }
+    if (sel.cnt_eq != sel.need_eq) {  // ties at the threshold: lowest slots first
+      int tot;
+      int r = block_exclusive_scan(__popc(eqmask), scratch, &tot);
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e)
+        if ((eqmask >> e) & 1u) {
+          if (r < sel.need_eq) vmask |= 1u << e;
+          ++r;
+        }
+    } else {
+      vmask |= eqmask;
+    }
+  }
+  int tot;
+  int pos = block_exclusive_scan(__popc(vmask), scratch, &tot);
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e)
+    if ((vmask >> e) & 1u) {
+      if (pos < m) vslot[pos] = i0 + e;
+      ++pos;
+    }
+  __syncthreads();
+  return tot < m ? tot : m;
+}
+
 // ---------------------------------------------------------------------------
 // Top-2048 threshold of one (request, query) score row, written to the
 // workspace for a management kernel (MTP3, and MTP0 sources longer than the
@@ -1169,9 +1254,11 @@ __global__ __launch_bounds__(kManageThreads) void lim_mtp_victims_kernel(LimArgs
   for (int p = tid; p < parts; p += kManageThreads)
     local += counts[p * 8 + 0] + counts[p * 8 + 1] + counts[p * 8 + 2] + counts[p * 8 + 3];
   const int m = block_sum(local, scratch);  // union misses
-  const int nv = select_victims(c, m, w.slot_table + static_cast<int64_t>(b) * kTableStride,
-                                w.slot_key + static_cast<int64_t>(b) * kTableStride,
-                                w.vslot + static_cast<int64_t>(b) * kUnionCap, hist, scratch, bcast, red);
+  const uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  const uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
+  int32_t* vslot = w.vslot + static_cast<int64_t>(b) * kUnionCap;
+  const int nv = c <= 16 * kManageThreads ? select_victims_regs<16>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
+                                          : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
   if (tid == 0) {
     w.nvict[b] = nv;
     a.miss_counts[b] = m;
