@@ -41,6 +41,11 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-unit additions.  lim.hip: MFMA results in VGPRs (the score epilogue reads
+# every accumulator; in AGPRs each one costs an extra v_accvgpr_read).
+EXTRA_FLAGS = {"lim.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -49,7 +54,7 @@ def _hipcc() -> str:
 
 
 def _compile(hipcc: str, src: Path, obj: Path) -> None:
-    cmd = [hipcc, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")

@@ -207,7 +207,11 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
           acc = T::mfma32(__builtin_bit_cast(typename T::vec8, qa[ks]),
                           __builtin_bit_cast(typename T::vec8, kb[tt][ks]), acc);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) part[tt] += wv[i] * (RELU ? fmaxf(acc[i], 0.f) : acc[i]);
+        // ReLU as a signed-integer max on the bit pattern: negative floats
+        // (and -0) are negative integers.  fmaxf would also quiet NaNs,
+        // one extra instruction per element.
+        for (int i = 0; i < 16; ++i)
+          part[tt] += wv[i] * (RELU ? __int_as_float(max(__float_as_int(acc[i]), 0)) : acc[i]);
       }
     }
 #pragma unroll
