@@ -137,40 +137,65 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
   const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kScoreWaves;
   if (col0 * kBlock >= n) return;
 
-  // Stage the request's Q*HEADS query rows (16 x 16-byte chunks each) and weights.
-  const uint4* qsrc = static_cast<const uint4*>(a.query) + static_cast<int64_t>(b) * Q * HEADS * 16;
-  for (int i = threadIdx.x; i < Q * HEADS * 16; i += blockDim.x) {
-    const int row = i >> 4, chunk = i & 15;
-    *reinterpret_cast<uint4*>(&qs[row * kQStride + chunk * 8]) = qsrc[i];
-  }
-  const uint16_t* wsrc = static_cast<const uint16_t*>(a.weights) + static_cast<int64_t>(b) * Q * HEADS;
-  for (int i = threadIdx.x; i < Q * HEADS; i += blockDim.x) ws[i] = T::to_float(wsrc[i]);
-  __syncthreads();
-
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 5;   // k-half of the MFMA operand
   const int col_lane = lane & 31;
   const int64_t col = col0 + wave;
   const int64_t t0 = col * kBlock;
-  if (t0 >= n) return;
+  const bool has_block = t0 < n;
+  const int32_t phys = has_block ? a.block_table[static_cast<int64_t>(b) * a.cols + col] : -1;
+  const bool key_ok = has_block && phys >= 0 && phys < a.key_blocks;
+
+  // Prologue, every load issued before any is waited on and with no branch
+  // between them (a branch makes the load-counter waits after it count the
+  // slowest path): the request's Q*HEADS query rows (16 x 16-byte chunks
+  // each) and weights into registers, then the wave's key block (128 rows of
+  // 256 bytes), each key load instruction reading 4 whole rows (16 lanes per
+  // row).  The query rows go to LDS once their (earlier) loads land, while
+  // the key loads are still in flight.  The key block is read through a
+  // buffer resource whose range is empty for an unmapped block, so those
+  // loads return zeros instead of needing a branch.  (Loading the MFMA
+  // operand layout directly -- 32 rows x 32 bytes per instruction -- has the
+  // L2 fetch ~1.4x the block's bytes from HBM.  Native vector types: uint4
+  // struct copies of these arrays stay in scratch memory.)
+  constexpr int kThreads = kScoreWaves * kWave;
+  constexpr int kQLoads = Q * HEADS * 16 / kThreads;
+  static_assert(Q * HEADS * 16 % kThreads == 0 && Q * HEADS <= kThreads, "score staging layout");
+  const u32x4_t* qsrc = static_cast<const u32x4_t*>(a.query) + static_cast<int64_t>(b) * Q * HEADS * 16;
+  u32x4_t qv[kQLoads];
+#pragma unroll
+  for (int k = 0; k < kQLoads; ++k) qv[k] = qsrc[k * kThreads + threadIdx.x];
+  const uint16_t w16 = static_cast<const uint16_t*>(a.weights)[static_cast<int64_t>(b) * Q * HEADS +
+                                                                threadIdx.x % (Q * HEADS)];
+  const char* kbase = static_cast<const char*>(a.key_cache) + (key_ok ? static_cast<int64_t>(phys) * kBlock * 256 : 0);
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbase), 0, key_ok ? kBlock * 256 : 0, kBufferFlags);
+  u32x4_t raw[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i)  // row 4i + lane/16, chunk lane%16
+    raw[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (i * kWave + lane) * 16, 0, 0);
+#pragma unroll
+  for (int k = 0; k < kQLoads; ++k) {
+    const int i = k * kThreads + threadIdx.x;
+    *reinterpret_cast<u32x4_t*>(&qs[(i >> 4) * kQStride + (i & 15) * 8]) = qv[k];
+  }
+  if (threadIdx.x < Q * HEADS) ws[threadIdx.x] = T::to_float(w16);
+  // Only LDS needs ordering here; a full __syncthreads() fence would also
+  // wait for the key loads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+  if (!has_block) return;
   const int64_t cap = a.source_capacity;
   float* srow = scores + static_cast<int64_t>(b) * Q * cap;
-  const int32_t phys = a.block_table[static_cast<int64_t>(b) * a.cols + col];
-  if (phys < 0 || phys >= a.key_blocks) {
+  if (!key_ok) {
     for (int q = 0; q < Q; ++q)
       for (int j = lane; j < kBlock; j += kWave)
         if (t0 + j < n) srow[q * cap + t0 + j] = -FLT_MAX;
     return;
   }
-  // Key block (128 rows of 256 bytes): each load instruction reads 4 whole
-  // rows (16 lanes per row), all 32 issued first.  (Loading the MFMA operand
-  // layout directly -- 32 rows x 32 bytes per instruction -- has the L2 fetch
-  // ~1.4x the block's bytes from HBM.)
-  const uint4* kp = static_cast<const uint4*>(a.key_cache) + static_cast<int64_t>(phys) * kBlock * 16;
-  uint4 raw[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) raw[i] = kp[i * kWave + lane];  // row 4i + lane/16, chunk lane%16
   // Per 32-token tile, a transpose through the wave's own LDS rows into the
   // operand layout: kb[tt][ks] = chunk 2ks+grp of row 32tt+col_lane.  Only
   // this wave touches these rows.  A wave's LDS operations are performed in
@@ -182,7 +207,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) st[(4 * j + (lane >> 4)) * kStageStride + (lane & 15)] = raw[tt * 8 + j];
+    for (int j = 0; j < 8; ++j) st[(4 * j + (lane >> 4)) * kStageStride + (lane & 15)] = __builtin_bit_cast(uint4, raw[tt * 8 + j]);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) kb[tt][ks] = st[col_lane * kStageStride + ks * 2 + grp];
   }

@@ -31,6 +31,12 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Word 3 of a raw (unformatted, stride 0) buffer resource on CDNA: DATA_FORMAT
+// = 32 bit, everything else zero.  A buffer load whose byte offset falls
+// outside the resource's num_records returns zeros and touches no memory.
+constexpr int kBufferFlags = 0x00020000;
 
 // Element type tags: storage is 16-bit either way; MFMA flavour differs.
 struct Bf16 {

@@ -39,7 +39,9 @@ HIP kernels implement:
   MTP3: ordered-union order);
 * an attention key whose slot is negative, >= the visible length, or does
   not resolve through the block table is left out of the softmax;
-* first-decode init gives slot i to the i-th smallest selected token.
+* first-decode init gives slot i to the i-th smallest selected token;
+* an index block-table entry that names no key block scores its tokens
+  -FLT_MAX (the reference reads that memory unchecked).
 
 Parity unpinned (no reference test or vector fixes them): the reference's own
 victim choice and in-row order where they differ from the rules above, and
@@ -112,6 +114,29 @@ def gather_rows(cache: np.ndarray, table_row: np.ndarray, n: int) -> np.ndarray:
     phys = np.asarray(table_row)[cols].astype(np.int64)
     flat = cache.reshape(cache.shape[0], BLOCK, -1)
     return flat[phys, offs]
+
+
+def index_scores_paged(query: np.ndarray, weights: np.ndarray, key_cache: np.ndarray, table_row: np.ndarray,
+                       n: int, score_fn=None) -> np.ndarray:
+    """Scores of logical tokens [0, n) whose keys sit in a paged cache.
+
+    A block-table entry that names no block (negative, or >= the cache's
+    block count) gives its tokens the score -FLT_MAX, below every real
+    score and above a free slot's victim key (-inf).  The reference reads
+    such an entry's memory unchecked (fused_li_manage_service_cube.h:217);
+    the guard is this build's own, and the HIP score kernels write the same
+    value.
+    """
+    table_row = np.asarray(table_row)
+    blocks = key_cache.shape[0]
+    phys = table_row[np.arange(n) // BLOCK].astype(np.int64)
+    bad = (phys < 0) | (phys >= blocks)
+    safe = table_row.copy()
+    safe[(safe < 0) | (safe >= blocks)] = 0
+    keys = gather_rows(key_cache, safe, n)
+    s = (score_fn or index_scores)(query, weights, keys)
+    s[bad] = -float(np.finfo(np.float32).max)
+    return s
 
 
 def topk_mask(scores: np.ndarray, k: int) -> np.ndarray:
@@ -212,8 +237,7 @@ def fused_li_manage(query, weights, key_cache, block_table, num_candidates, num_
             if scores is not None:
                 scores.append(None)
             continue
-        keys = gather_rows(kc, block_table[b], n)
-        s = index_scores(q[b], w[b], keys)
+        s = index_scores_paged(q[b], w[b], kc, block_table[b], n)
         if scores is not None:
             scores.append(s)
         src, dst, m = lim_manage_row(s, pool[r], n, c)
@@ -283,8 +307,8 @@ def fused_li_manage_mtp(query, weights, key_cache, block_table, num_candidates, 
             if scores is not None:
                 scores.append(None)
             continue
-        keys = gather_rows(kc, block_table[b], n)
-        s4 = np.stack([index_scores(q[MTP_Q * b + j], w[MTP_Q * b + j], keys) for j in range(MTP_Q)])
+        s4 = np.stack([index_scores_paged(q[MTP_Q * b + j], w[MTP_Q * b + j], kc, block_table[b], n)
+                       for j in range(MTP_Q)])
         if scores is not None:
             scores.append(s4)
         rs, rd, ms, md = lim_manage_mtp_row(s4, pool[r], n, c)
@@ -370,8 +394,8 @@ def initialize_lidu_row(query, weights, key_cache, index_table_row, candidate_le
     if c <= 0:
         return None
     _lidu_init_checks(n, c)
-    keys = gather_rows(bits_to_f32(key_cache, dtype), np.asarray(index_table_row), n)
-    scores = linear_index_scores(bits_to_f32(query, dtype), bits_to_f32(weights, dtype), keys)
+    scores = index_scores_paged(bits_to_f32(query, dtype), bits_to_f32(weights, dtype), bits_to_f32(key_cache, dtype),
+                                index_table_row, n, score_fn=linear_index_scores)
     sel = np.nonzero(topk_mask(scores, c))[0].astype(np.int32)
     slots = np.arange(c, dtype=np.int32)
     slots_row[:] = -1

@@ -211,6 +211,10 @@ def test_lim_ties_at_threshold_bit_exact(mtp, positives):
     expect = oracle_lim(case, mtp=mtp)
     d = case.to_device("cuda", host_mapped=False)
     _run_lim(d, mtp=mtp)
+    _assert_matches(d, expect, mtp)
+
+
+def _assert_matches(d, expect, mtp):
     mc = ints(d["miss_counts"])
     assert np.array_equal(mc, expect["miss_counts"])
     assert np.array_equal(ints(d["topk_src_ids"]), expect["src"])
@@ -221,6 +225,29 @@ def test_lim_ties_at_threshold_bit_exact(mtp, positives):
             assert np.array_equal(ms[b, :mc[b]], expect["miss_src"][b, :mc[b]])
             assert np.array_equal(md[b, :mc[b]], expect["miss_dst"][b, :mc[b]])
     assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
+
+
+@pytest.mark.parametrize("mtp,positives", [(False, [700]), (True, [500, 900, 1300, 1900])])
+def test_lim_unmapped_index_blocks_score_lowest(mtp, positives):
+    """Index block-table entries that name no key block (-1, or at or past
+    the cache's block count) score -FLT_MAX: below every real score, above
+    a free slot when victims are ranked.  The reference reads such an
+    entry's memory unchecked (fused_li_manage_service_cube.h:217), so this
+    is this library's own guard, restated by the oracle.  One unmapped block
+    in the zero-score tie region (block 0), others above it."""
+    case = _tie_case(mtp, positives)
+    t = case.tensors
+    table = t["index_block_table"]
+    nblk = t["index_key_cache"].shape[0]
+    n = ints(t["num_candidate_tokens"])
+    picks = [(0, (int(n[0]) - 1) // 128, -1), (1, int(n[1]) // 256, nblk), (2, int(n[2]) // 192, nblk + 7), (2, 0, -5)]
+    for b, col, bad in picks:
+        table[b, col] = bad
+    print(f"LIM unmapped index blocks mtp={mtp} picks={picks}", flush=True)
+    expect = oracle_lim(case, mtp=mtp)
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d, mtp=mtp)
+    _assert_matches(d, expect, mtp)
 
 
 def test_lim_row_guards():

@@ -107,6 +107,45 @@ def test_gather_rows_follows_block_table():
     assert np.array_equal(rows[129], cache[0, 1, 0])
 
 
+def test_paged_scores_unmapped_blocks():
+    """Tokens of a block-table entry that names no block score -FLT_MAX;
+    the rest equal the brute-force scores of the rows the entry names."""
+    rng = np.random.default_rng(2)
+    cache = rng.standard_normal((4, 128, 1, 8))
+    q = rng.standard_normal((3, 8))
+    w = rng.standard_normal(3)
+    table = np.array([3, -1, 1, 4, 0, 2])  # -1 and 4 (== block count) name no block
+    n = 5 * 128 + 17
+    s = O.index_scores_paged(q, w, cache, table, n)
+    flt_max = float(np.finfo(np.float32).max)
+    for t in range(n):
+        phys = table[t // 128]
+        if phys < 0 or phys >= 4:
+            assert s[t] == -flt_max
+        else:
+            k = cache[phys, t % 128, 0]
+            assert np.isclose(s[t], sum(w[h] * max(0.0, float(q[h] @ k)) for h in range(3)), rtol=1e-12, atol=1e-12)
+
+
+def test_unmapped_block_tokens_rank_after_free_slots_before_scored():
+    # n = 2300, C = 2049: two misses.  Slots 0..2045 hold hits; slot 2048 is
+    # free; token 0 (slot 2047) sits in an unmapped block (-FLT_MAX); token
+    # 128 (slot 2046) scores 0.  Victims: the free slot and token 0's slot.
+    n, c = 2300, 2049
+    scores = np.arange(n, dtype=np.float64)
+    scores[:128] = -float(np.finfo(np.float32).max)  # block 0 unmapped
+    scores[128] = 0.0
+    row = np.full(n, -1, np.int64)
+    top = np.arange(n - TOPK, n)
+    row[top[2:]] = np.arange(TOPK - 2)
+    row[128] = 2046
+    row[0] = 2047
+    src, dst, m = O.lim_manage_row(scores, row, n, c)
+    assert m == 2 and src[:2].tolist() == top[:2].tolist()
+    assert dst[:2].tolist() == [2047, 2048]
+    assert row[0] == -1 and row[128] == 2046
+
+
 # --------------------------------------------------------------------------
 # top-k
 def test_topk_closed_form_last_ids():
