@@ -504,31 +504,67 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_mtp_overlap_kernel(SfaArgs a
   sfa_split_body<T, false, kKeysResident>(a, part, splits, 0, splits_total, i % attn_blocks, i / attn_blocks);
 }
 
-// Merge split partials: one 128-thread workgroup per (row, head), 4 dims per thread.
-template <typename T>
+// Merge split partials: one 128-thread workgroup per (row, head), 4 dims per
+// thread.  MAXS > 0 (splits <= MAXS): every split's (m, l) and output slice
+// are loaded at once -- an index past the last split rereads the last one
+// and is ignored -- so the merge waits on one round of loads instead of two
+// dependent ones.  MAXS == 0 loops over any number of splits.  Both sum in
+// split order, so they round identically.
+template <typename T, int MAXS>
 __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
   const int64_t row = blockIdx.x;
   const int head = blockIdx.y;
   const int64_t H = a.heads;
   float mmax = -INFINITY;
-  for (int s = 0; s < splits; ++s) {
-    const int64_t pidx = (row * splits + s) * H + head;
-    if (part.ml[pidx * 2 + 1] > 0.f) mmax = fmaxf(mmax, part.ml[pidx * 2]);
-  }
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   float total = 0.f;
-  if (mmax != -INFINITY) {
+  if constexpr (MAXS > 0) {
+    float2 ml[MAXS];
+    float4 o[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+      const int64_t pidx = (row * splits + (s < splits ? s : splits - 1)) * H + head;
+      ml[s] = reinterpret_cast<const float2*>(part.ml)[pidx];
+      o[s] = reinterpret_cast<const float4*>(part.o + pidx * kCkvDim)[threadIdx.x];
+    }
+    // Consumed here, unconditionally: otherwise the compiler sinks each
+    // split's loads into its conditional use below, one wait each.
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s)
+      asm volatile("" : "+v"(ml[s].x), "+v"(ml[s].y), "+v"(o[s].x), "+v"(o[s].y), "+v"(o[s].z), "+v"(o[s].w));
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s)
+      if (s < splits && ml[s].y > 0.f) mmax = fmaxf(mmax, ml[s].x);
+    if (mmax != -INFINITY) {
+#pragma unroll
+      for (int s = 0; s < MAXS; ++s) {
+        if (!(s < splits && ml[s].y > 0.f)) continue;
+        const float w = exp2f(ml[s].x - mmax);
+        total += ml[s].y * w;
+        acc.x += o[s].x * w;
+        acc.y += o[s].y * w;
+        acc.z += o[s].z * w;
+        acc.w += o[s].w * w;
+      }
+    }
+  } else {
     for (int s = 0; s < splits; ++s) {
       const int64_t pidx = (row * splits + s) * H + head;
-      const float l = part.ml[pidx * 2 + 1];
-      if (!(l > 0.f)) continue;
-      const float w = exp2f(part.ml[pidx * 2] - mmax);
-      total += l * w;
-      const float4 o = reinterpret_cast<const float4*>(part.o + pidx * kCkvDim)[threadIdx.x];
-      acc.x += o.x * w;
-      acc.y += o.y * w;
-      acc.z += o.z * w;
-      acc.w += o.w * w;
+      if (part.ml[pidx * 2 + 1] > 0.f) mmax = fmaxf(mmax, part.ml[pidx * 2]);
+    }
+    if (mmax != -INFINITY) {
+      for (int s = 0; s < splits; ++s) {
+        const int64_t pidx = (row * splits + s) * H + head;
+        const float l = part.ml[pidx * 2 + 1];
+        if (!(l > 0.f)) continue;
+        const float w = exp2f(part.ml[pidx * 2] - mmax);
+        total += l * w;
+        const float4 o = reinterpret_cast<const float4*>(part.o + pidx * kCkvDim)[threadIdx.x];
+        acc.x += o.x * w;
+        acc.y += o.y * w;
+        acc.z += o.z * w;
+        acc.w += o.w * w;
+      }
     }
   }
   const float inv = total > 0.f ? 1.f / total : 0.f;
@@ -538,6 +574,17 @@ __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials pa
   const uint32_t hi = static_cast<uint32_t>(T::from_float(acc.z * inv)) |
                       (static_cast<uint32_t>(T::from_float(acc.w * inv)) << 16);
   *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
+}
+
+constexpr int kCombineMaxS = 8;
+
+template <typename T>
+void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int splits, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads));
+  if (splits <= kCombineMaxS)
+    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, kCombineMaxS>, grid, dim3(128), stream, a, p, splits);
+  else
+    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, 0>, grid, dim3(128), stream, a, p, splits);
 }
 
 template <typename T, bool FUSED>
@@ -553,8 +600,7 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
                 stream, args, p, splits, 0, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>,
-                dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads)), dim3(128), stream, a, p, splits);
+  launch_combine<T>(a, p, rows, splits, stream);
   return hipGetLastError();
 }
 
@@ -596,8 +642,7 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
                 p, s2, s1, total);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>,
-                dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads)), dim3(128), stream, a, p, total);
+  launch_combine<T>(a, p, rows, total, stream);
   return hipGetLastError();
 }
 
