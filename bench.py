@@ -361,6 +361,7 @@ def main() -> int:
         rows["cfg3_mtp3"] = measure_mtp3(torch, np, dev, args.seed)
         rows["cfg2_bs64_mixed"] = measure_cfg2(torch, np, dev, args.seed)
         rows["lidu_init"] = measure_lidu_init(torch, np, dev, args.seed)
+        rows["indexer_project"] = measure_indexer(torch, dev, args.seed)
 
     value_us = graph_ms * 1000.0
     line = {
@@ -612,6 +613,71 @@ def measure_lidu_init(torch, np, dev, seed: int, reps: int = 5):
     del keys, dkpe, dckv
     torch.cuda.empty_cache()
     return out
+
+
+def measure_indexer(torch, dev, seed: int, reps: int = 20):
+    """Decode indexer projection at the GLM indexer's shapes (hidden 6144,
+    q_lora_rank 2048, 32 heads x 128, rope 64) for the cfg1 batch of 24
+    tokens: the fused launch (q projection + RoPE + head weights) against
+    the same work as two library GEMMs plus the RoPE kernel."""
+    import torch.nn.functional as F
+
+    from nanovllm_amd import _lib
+    from nanovllm_amd import ops
+    from nanovllm_amd.dsa_indexer_project import dsa_indexer_project_query_only
+
+    T, HID, R, H, D, ROPE = 24, 6144, 2048, 32, 128, 64
+    g = torch.Generator().manual_seed(seed)
+    bf = torch.bfloat16
+    hidden = torch.randn(T, HID, generator=g).to(bf).to(dev)
+    qc = torch.randn(T, R, generator=g).to(bf).to(dev)
+    wq = (torch.randn(H * D, R, generator=g) / R ** 0.5).to(bf).to(dev)
+    wp = (torch.rand(H, HID, generator=g) / HID ** 0.5).to(bf).to(dev)
+    ang = torch.arange(1, T + 1).float()[:, None] * torch.linspace(0.01, 0.4, ROPE // 2)[None, :]
+    cos = ang.cos().repeat_interleave(2, -1).to(bf).view(T, 1, 1, ROPE).to(dev)
+    sin = ang.sin().repeat_interleave(2, -1).to(bf).view(T, 1, 1, ROPE).to(dev)
+    q_out = torch.empty(T, H, D, dtype=bf, device=dev)
+    w_out = torch.empty(T, H, dtype=bf, device=dev)
+
+    def fused():
+        dsa_indexer_project_query_only(hidden, qc, cos, sin, wq, wp, q_out, w_out, n_head=H, head_dim=D,
+                                       rope_dim=ROPE, score_scale=1.0)
+
+    def library():
+        q = F.linear(qc, wq).view(T, H, D)
+        w_out.copy_(F.linear(hidden, wp))
+        ops.dsa_indexer_query_rope_inplace(q, cos, sin, ROPE)
+        return q
+
+    fused()
+    library()
+    torch.cuda.synchronize()
+    with _lib.KernelTimer(capacity=4 * reps) as kt:
+        for _ in range(reps):
+            fused()
+        torch.cuda.synchronize()
+    k_us = kt.mean_ms("indexer_project_kernel") * 1000.0
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for fn in (fused, library):
+        for _ in range(3):
+            fn()
+        ev0.record()
+        for _ in range(reps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        if fn is fused:
+            fused_us = ev0.elapsed_time(ev1) * 1000.0 / reps
+        else:
+            lib_us = ev0.elapsed_time(ev1) * 1000.0 / reps
+    weight_bytes = (H * D * R + H * HID) * 2
+    act_bytes = T * (R + HID) * 2 + T * H * (D + 1) * 2 + 2 * T * ROPE * 2
+    algo = weight_bytes + act_bytes
+    return {"workload": f"T={T} tokens, hidden {HID}, q_lora_rank {R}, {H} heads x {D}, rope {ROPE}, bf16",
+            "kernel_us": round(k_us, 2), "algorithmic_bytes": algo,
+            "hbm_GBs": round(algo / (k_us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(algo / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+            "fused_call_us": round(fused_us, 2), "library_gemms_plus_rope_us": round(lib_us, 2)}
 
 
 def cpu_baseline(case, queries_cpu, steps: int):

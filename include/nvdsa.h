@@ -3,7 +3,9 @@
  *
  * Seven entry points replace the seven torch.library operators that the
  * reference registers under the `nanovllm_dsa` namespace
- * (reference: csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:645-696).
+ * (reference: csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:645-696);
+ * further ones cover the first-decode initialisation and the decode
+ * indexer projection that produces the LIM inputs.
  * Each takes its arguments in the same order as the reference schema, as
  * plain tensor descriptors (device address + dtype + shape), plus the HIP
  * stream to launch on.  Every entry point:
@@ -277,6 +279,48 @@ int nvdsa_initialize_lidu_row_shared(const nvdsa_tensor* cache_slots_row,
                                      const nvdsa_tensor* dram_block_table,
                                      void* workspace, size_t workspace_bytes,
                                      void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* In-place interleaved-pair RoPE of the first rope_dim dims of every
+ * [token, head] row of q_inout [T, H, D] (16-bit); cos/sin [T, 1, 1, rope_dim]
+ * of the same dtype, token t's values at t * rope_dim.  Per pair (even,
+ * odd): even' = even*cos - odd*sin, odd' = odd*cos + even*sin, each product
+ * and the sum rounded in fp32, then rounded to nearest even.
+ * Replaces torch.ops.nanovllm_dsa.dsa_indexer_query_rope_inplace
+ * (reference csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:713-714;
+ * checks ops/dsa_indexer_project/dsa_indexer_project_torch_adpt.h:42-90;
+ * kernel ops/dsa_indexer_project/op_kernel/dsa_indexer_project_kernel.cpp:60-176). */
+int nvdsa_dsa_indexer_query_rope_inplace(const nvdsa_tensor* q_inout,
+                                         const nvdsa_tensor* cos,
+                                         const nvdsa_tensor* sin,
+                                         int64_t rope_dim,
+                                         void* stream);
+
+/* Decode indexer projection in one launch:
+ *   q_index_out[t]       = RoPE(round16(q_c[t] . wq_b_weight^T)) viewed [n_head, head_dim]
+ *   index_weights_out[t] = round16(round16(hidden_states[t] . weights_proj_weight^T) * score_scale)
+ * (the second rounding only when score_scale != 1).  Replaces the
+ * PyTorch function dsa_indexer_project_query_only
+ * (reference nanovllm/models/dsa_indexer_project.py:296-355) for the case
+ * where weights_proj_weight shares the activations' 16-bit dtype; pass both
+ * weights_proj_weight and index_weights_out as NULL to compute q only.
+ * cos/sin hold numel/T >= rope_dim values per token (the reference's
+ * reshape(T, -1)[..., :rope_dim], :28-32).  Limits of this implementation:
+ * q_lora_rank a multiple of 256, hidden_size of 512, n_head and head_dim
+ * multiples of 16.  No workspace. */
+int nvdsa_dsa_indexer_project_query_only(const nvdsa_tensor* hidden_states,
+                                         const nvdsa_tensor* q_c,
+                                         const nvdsa_tensor* cos,
+                                         const nvdsa_tensor* sin,
+                                         const nvdsa_tensor* wq_b_weight,
+                                         const nvdsa_tensor* weights_proj_weight,
+                                         const nvdsa_tensor* q_index_out,
+                                         const nvdsa_tensor* index_weights_out,
+                                         int64_t n_head,
+                                         int64_t head_dim,
+                                         int64_t rope_dim,
+                                         double score_scale,
+                                         void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Pinned, device-mapped host memory for the DRAM KV caches: the counterpart

@@ -63,7 +63,16 @@ bool is_half(const nvdsa_tensor* t) {
 bool aligned16(const nvdsa_tensor* t) {
   return numel(t) == 0 || (reinterpret_cast<uintptr_t>(t->data) & 15u) == 0;
 }
+bool aligned4(const nvdsa_tensor* t) {
+  return numel(t) == 0 || (reinterpret_cast<uintptr_t>(t->data) & 3u) == 0;
+}
 bool has_data(const nvdsa_tensor* t) { return numel(t) == 0 || t->data != nullptr; }
+// A shape as Python prints a tuple: "(24, 32, 128)", "(24,)".
+std::string shape_str(const nvdsa_tensor* t) {
+  std::string out = "(";
+  for (int i = 0; i < t->ndim; ++i) out += (i ? ", " : "") + std::to_string(t->shape[i]);
+  return out + (t->ndim == 1 ? ",)" : ")");
+}
 
 nvdsa::Elem elem_of(const nvdsa_tensor* t) {
   return t->dtype == NVDSA_BFLOAT16 ? nvdsa::Elem::kBf16 : nvdsa::Elem::kF16;
@@ -172,7 +181,8 @@ const char* nvdsa_kernel_name(int32_t kernel_id) {
                                 "lim_mtp_pass_a_kernel", "sfa_split_kernel", "sfa_split_kernel_fused",
                                 "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel",
                                 "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
-                                "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied"};
+                                "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied", "indexer_project_kernel",
+                                "indexer_rope_kernel"};
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }
@@ -858,6 +868,140 @@ int nvdsa_fused_copy_sfa_mtp(const nvdsa_tensor* query_rope, const nvdsa_tensor*
   return run_fused("fused_copy_sfa_mtp", t, nvdsa::kMtpQueries, topk_src_ids, miss_src_ids, miss_dst_slots,
                    miss_counts, dram_block_table, dram_k_rope, dram_kv_cache, scale_value, workspace,
                    workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------------
+int nvdsa_dsa_indexer_query_rope_inplace(const nvdsa_tensor* q_inout, const nvdsa_tensor* cos,
+                                         const nvdsa_tensor* sin, int64_t rope_dim, void* stream) {
+  const nvdsa_tensor* const all[] = {q_inout, cos, sin};
+  if (!all_nonnull(all)) return fail(NVDSA_ERR_ARG, "dsa_indexer_query_rope_inplace: null tensor argument");
+  Check c("dsa_indexer_query_rope_inplace");
+  // ops/dsa_indexer_project/dsa_indexer_project_torch_adpt.h:31-90, in its order.
+  c.need(dims_are(q_inout, 3), NVDSA_ERR_SHAPE, "q_inout rank mismatch.")
+      .need(q_inout->contiguous == 1, NVDSA_ERR_LAYOUT, "q_inout must be contiguous.")
+      .need(cos->dtype == q_inout->dtype, NVDSA_ERR_DTYPE, "cos dtype mismatch.")
+      .need(dims_are(cos, 4), NVDSA_ERR_SHAPE, "cos rank mismatch.")
+      .need(cos->contiguous == 1, NVDSA_ERR_LAYOUT, "cos must be contiguous.")
+      .need(sin->dtype == q_inout->dtype, NVDSA_ERR_DTYPE, "sin dtype mismatch.")
+      .need(dims_are(sin, 4), NVDSA_ERR_SHAPE, "sin rank mismatch.")
+      .need(sin->contiguous == 1, NVDSA_ERR_LAYOUT, "sin must be contiguous.")
+      .need(is_half(q_inout), NVDSA_ERR_DTYPE, "q_inout must be float16 or bfloat16.")
+      .need(q_inout->device == cos->device && q_inout->device == sin->device && q_inout->device >= 0,
+            NVDSA_ERR_DEVICE, "q_inout, cos and sin must be on the same GPU.");
+  if (c.ok()) {
+    const int64_t T = sz(q_inout, 0), H = sz(q_inout, 1), D = sz(q_inout, 2);
+    c.need(T > 0 && H > 0 && D > 0, NVDSA_ERR_SHAPE, "q_inout must be non-empty.")
+        .need(sz(cos, 0) == T && sz(sin, 0) == T, NVDSA_ERR_SHAPE, "cos/sin token dimension mismatch.")
+        .need(numel(cos) >= T * rope_dim && numel(sin) >= T * rope_dim, NVDSA_ERR_SHAPE,
+              "cos/sin storage is smaller than num_tokens * rope_dim.")
+        .need(rope_dim > 0 && rope_dim <= D && rope_dim % 16 == 0, NVDSA_ERR_ARG,
+              "rope_dim must be positive, no larger than head_dim, and aligned to 16.")
+        .need(D <= 256 && D % 16 == 0 && H <= 128, NVDSA_ERR_SHAPE,
+              "query RoPE requires head_dim <= 256 aligned to 16 and n_head <= 128.")
+        .need(has_data(q_inout) && has_data(cos) && has_data(sin), NVDSA_ERR_ARG, "null data pointer")
+        .need(aligned4(q_inout) && aligned4(cos) && aligned4(sin), NVDSA_ERR_LAYOUT,
+              "q_inout, cos and sin must be 4-byte aligned");
+  }
+  if (!c.ok()) return c.finish();
+  nvdsa::RopeArgs a{};
+  a.q = q_inout->data;
+  a.cos = cos->data;
+  a.sin = sin->data;
+  a.heads = sz(q_inout, 1);
+  a.rows = sz(q_inout, 0) * a.heads;
+  a.head_dim = sz(q_inout, 2);
+  a.rope_dim = rope_dim;
+  a.elem = elem_of(q_inout);
+  return launch_status(nvdsa::launch_indexer_rope(a, static_cast<hipStream_t>(stream)),
+                       "dsa_indexer_query_rope_inplace");
+}
+
+int nvdsa_dsa_indexer_project_query_only(const nvdsa_tensor* hidden_states, const nvdsa_tensor* q_c,
+                                         const nvdsa_tensor* cos, const nvdsa_tensor* sin,
+                                         const nvdsa_tensor* wq_b_weight, const nvdsa_tensor* weights_proj_weight,
+                                         const nvdsa_tensor* q_index_out, const nvdsa_tensor* index_weights_out,
+                                         int64_t n_head, int64_t head_dim, int64_t rope_dim, double score_scale,
+                                         void* stream) {
+  const nvdsa_tensor* const req[] = {hidden_states, q_c, cos, sin, wq_b_weight, q_index_out};
+  if (!all_nonnull(req)) return fail(NVDSA_ERR_ARG, "dsa_indexer_project_query_only: null tensor argument");
+  if ((weights_proj_weight == nullptr) != (index_weights_out == nullptr))
+    return fail(NVDSA_ERR_ARG,
+                "dsa_indexer_project_query_only: weights_proj_weight and index_weights_out go together");
+  const bool with_w = weights_proj_weight != nullptr;
+  const int64_t T = sz(hidden_states, 0);
+  // The reference's output checks (nanovllm/models/dsa_indexer_project.py:316-319).
+  if (!(dims_are(q_index_out, 3) && sz(q_index_out, 0) == T && sz(q_index_out, 1) == n_head &&
+        sz(q_index_out, 2) == head_dim)) {
+    const std::string m = "q_index_out shape must be (" + std::to_string(T) + ", " + std::to_string(n_head) + ", " +
+                          std::to_string(head_dim) + "), got " + shape_str(q_index_out);
+    return fail(NVDSA_ERR_SHAPE, m.c_str());
+  }
+  if (with_w && !(dims_are(index_weights_out, 2) && sz(index_weights_out, 0) == T && sz(index_weights_out, 1) == n_head)) {
+    const std::string m = "index_weights_out shape must be (" + std::to_string(T) + ", " + std::to_string(n_head) +
+                          "), got " + shape_str(index_weights_out);
+    return fail(NVDSA_ERR_SHAPE, m.c_str());
+  }
+  Check c("dsa_indexer_project_query_only");
+  // This implementation's layout limits (projection shapes of
+  // nanovllm/models/dsa_indexer_project.py:93-104 and the GLM indexer,
+  // nanovllm/models/glm_mla.py:205-219).
+  const int64_t kc = nvdsa::indexer_k_chunk();
+  c.need(dims_are(hidden_states, 2) && dims_are(q_c, 2) && sz(q_c, 0) == T, NVDSA_ERR_SHAPE,
+         "hidden_states and q_c must be [tokens, features] with one row per token")
+      .need(dims_are(wq_b_weight, 2) && sz(wq_b_weight, 0) == n_head * head_dim && sz(wq_b_weight, 1) == sz(q_c, 1),
+            NVDSA_ERR_SHAPE, "wq_b_weight must be [n_head * head_dim, q_lora_rank]")
+      .need(!with_w || (dims_are(weights_proj_weight, 2) && sz(weights_proj_weight, 0) == n_head &&
+                        sz(weights_proj_weight, 1) == sz(hidden_states, 1)),
+            NVDSA_ERR_SHAPE, "weights_proj_weight must be [n_head, hidden_size]")
+      .need(n_head > 0 && n_head % 16 == 0 && head_dim > 0 && head_dim % 16 == 0, NVDSA_ERR_ARG,
+            "n_head and head_dim must be positive multiples of 16")
+      .need(rope_dim > 0 && rope_dim <= head_dim && rope_dim % 2 == 0, NVDSA_ERR_ARG,
+            "rope_dim must be positive, even and no larger than head_dim")
+      .need(sz(q_c, 1) > 0 && sz(q_c, 1) % kc == 0, NVDSA_ERR_SHAPE, "q_lora_rank must be a positive multiple of 256")
+      .need(!with_w || (sz(hidden_states, 1) > 0 && sz(hidden_states, 1) % 512 == 0), NVDSA_ERR_SHAPE,
+            "hidden_size must be a positive multiple of 512")
+      .need(is_half(hidden_states) && q_c->dtype == hidden_states->dtype && wq_b_weight->dtype == hidden_states->dtype &&
+                cos->dtype == hidden_states->dtype && sin->dtype == hidden_states->dtype &&
+                q_index_out->dtype == hidden_states->dtype &&
+                (!with_w || (weights_proj_weight->dtype == hidden_states->dtype &&
+                             index_weights_out->dtype == hidden_states->dtype)),
+            NVDSA_ERR_DTYPE, "all tensors must share one 16-bit dtype (fp16 or bf16)")
+      .need(T == 0 || (numel(cos) % T == 0 && numel(sin) == numel(cos) && numel(cos) / T >= rope_dim), NVDSA_ERR_SHAPE,
+            "cos/sin must hold at least rope_dim values per token");
+  if (c.ok()) {
+    check_common(c, req, hidden_states->device);
+    if (with_w) {
+      const nvdsa_tensor* const w2[] = {weights_proj_weight, index_weights_out};
+      check_common(c, w2, hidden_states->device);
+    }
+    c.need(hidden_states->device >= 0, NVDSA_ERR_DEVICE, "tensors must be on a GPU")
+        .need(aligned16(hidden_states) && aligned16(q_c) && aligned16(wq_b_weight) &&
+                  (!with_w || aligned16(weights_proj_weight)),
+              NVDSA_ERR_LAYOUT, "inputs and projection weights must be 16-byte aligned")
+        .need(aligned4(q_index_out) && aligned4(cos) && aligned4(sin) && (!with_w || aligned4(index_weights_out)),
+              NVDSA_ERR_LAYOUT, "outputs, cos and sin must be 4-byte aligned");
+  }
+  if (!c.ok()) return c.finish();
+  nvdsa::IndexerArgs a{};
+  a.hidden = hidden_states->data;
+  a.q_c = q_c->data;
+  a.cos = cos->data;
+  a.sin = sin->data;
+  a.wq_b = wq_b_weight->data;
+  a.w_proj = with_w ? weights_proj_weight->data : nullptr;
+  a.q_out = q_index_out->data;
+  a.w_out = with_w ? index_weights_out->data : nullptr;
+  a.tokens = T;
+  a.hid = sz(hidden_states, 1);
+  a.rank = sz(q_c, 1);
+  a.heads = n_head;
+  a.head_dim = head_dim;
+  a.rope_dim = rope_dim;
+  a.cos_stride = T > 0 ? numel(cos) / T : 0;
+  a.score_scale = static_cast<float>(score_scale);
+  a.elem = elem_of(hidden_states);
+  return launch_status(nvdsa::launch_indexer_project(a, static_cast<hipStream_t>(stream)),
+                       "dsa_indexer_project_query_only");
 }
 
 // ------------------------------------------------------------------------

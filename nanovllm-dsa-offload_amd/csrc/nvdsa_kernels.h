@@ -27,7 +27,9 @@ enum KernelId : int {
   kKernLimMtpPassB = 11,
   kKernSfaMtpOverlap = 12,
   kKernSfaSplitCopied = 13,
-  kKernCount = 14
+  kKernIdxProject = 14,
+  kKernIdxRope = 15,
+  kKernCount = 16
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.
@@ -172,5 +174,32 @@ struct SfaArgs {
 size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens);
 hipError_t launch_sparse_tail_attention(const SfaArgs& a, hipStream_t stream);
 hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream);
+
+// ---- indexer projection (decode query rows and head weights) -------------
+struct IndexerArgs {
+  const void* hidden;   // [tokens, hid]          16-bit
+  const void* q_c;      // [tokens, rank]
+  const void* cos;      // [tokens, cos_stride]   (first rope_dim used)
+  const void* sin;
+  const void* wq_b;     // [heads * head_dim, rank]
+  const void* w_proj;   // [heads, hid], or null: weights not computed here
+  void* q_out;          // [tokens, heads, head_dim]
+  void* w_out;          // [tokens, heads]
+  int64_t tokens, hid, rank, heads, head_dim, rope_dim, cos_stride;
+  float score_scale;
+  Elem elem;
+};
+// K extents (rank, hid) must be multiples of this.
+int64_t indexer_k_chunk();
+hipError_t launch_indexer_project(const IndexerArgs& a, hipStream_t stream);
+
+struct RopeArgs {
+  void* q;              // [rows = tokens * heads, head_dim], rotated in place
+  const void* cos;      // [tokens, rope_dim]
+  const void* sin;
+  int64_t rows, heads, head_dim, rope_dim;
+  Elem elem;
+};
+hipError_t launch_indexer_rope(const RopeArgs& a, hipStream_t stream);
 
 }  // namespace nvdsa

@@ -1,9 +1,9 @@
 """``torch.ops.nanovllm_dsa`` on PyTorch-ROCm, backed by libnvdsa.so.
 
-Importing this module registers the seven DSA offload operators under the
-reference's namespace and schemas (reference
-csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:645-696, registered on
-import by nanovllm/ops/__init__.py:38-50):
+Importing this module registers the seven DSA offload operators and the
+indexer's query RoPE under the reference's namespace and schemas (reference
+csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:645-696 and :713-714,
+registered on import by nanovllm/ops/__init__.py:38-50):
 
 * a CUDA-key implementation that hands plain tensor descriptors to the C ABI
   and launches on the current HIP stream (the counterpart of the PrivateUse1
@@ -92,6 +92,11 @@ SCHEMAS = {
         " Tensor(b!) hbm_kv_cache, Tensor dram_k_rope,"
         " Tensor dram_kv_cache, float scale_value,"
         " Tensor(c!) attention_out) -> ()"
+    ),
+    # nanovllm_ops.cpp:713-714
+    "dsa_indexer_query_rope_inplace": (
+        "dsa_indexer_query_rope_inplace(Tensor(a!) q_inout, Tensor cos,"
+        " Tensor sin, int rope_dim) -> ()"
     ),
 }
 
@@ -244,6 +249,25 @@ def lidu_init_row_shared(cache_slots_row, cache_tokens, hbm_kpe, hbm_ckv, dram_k
                                                    ws, wsn, _stream_of(hbm_kpe)))
 
 
+def _dsa_indexer_query_rope_inplace(q_inout, cos, sin, rope_dim) -> None:
+    descs = [_D(t) for t in (q_inout, cos, sin)]
+    _lib.check(_L.nvdsa_dsa_indexer_query_rope_inplace(*map(_ref, descs), int(rope_dim), _stream_of(q_inout)))
+
+
+def indexer_project_query_only(hidden_states, q_c, cos, sin, wq_b_weight, weights_proj_weight, q_index_out,
+                               index_weights_out, n_head, head_dim, rope_dim, score_scale) -> None:
+    """nvdsa_dsa_indexer_project_query_only on the current stream.  Pass
+    ``weights_proj_weight`` and ``index_weights_out`` as None to project q
+    only."""
+    descs = [_D(t) for t in (hidden_states, q_c, cos, sin, wq_b_weight)]
+    wp = _D(weights_proj_weight) if weights_proj_weight is not None else None
+    qo = _D(q_index_out)
+    wo = _D(index_weights_out) if index_weights_out is not None else None
+    _lib.check(_L.nvdsa_dsa_indexer_project_query_only(
+        *map(_ref, descs), _ref(wp) if wp is not None else None, _ref(qo), _ref(wo) if wo is not None else None,
+        int(n_head), int(head_dim), int(rope_dim), float(score_scale), _stream_of(q_c)))
+
+
 IMPLS = {
     "fused_li_manage": _fused_li_manage,
     "fused_li_manage_mtp": _fused_li_manage_mtp,
@@ -252,6 +276,7 @@ IMPLS = {
     "sparse_tail_attention_mtp": _sparse_tail_attention_mtp,
     "fused_copy_sfa": _fused_copy_sfa,
     "fused_copy_sfa_mtp": _fused_copy_sfa_mtp,
+    "dsa_indexer_query_rope_inplace": _dsa_indexer_query_rope_inplace,
 }
 
 
@@ -283,3 +308,4 @@ sparse_tail_attention = torch.ops.nanovllm_dsa.sparse_tail_attention.default
 sparse_tail_attention_mtp = torch.ops.nanovllm_dsa.sparse_tail_attention_mtp.default
 fused_copy_sfa = torch.ops.nanovllm_dsa.fused_copy_sfa.default
 fused_copy_sfa_mtp = torch.ops.nanovllm_dsa.fused_copy_sfa_mtp.default
+dsa_indexer_query_rope_inplace = torch.ops.nanovllm_dsa.dsa_indexer_query_rope_inplace.default

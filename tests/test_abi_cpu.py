@@ -20,7 +20,7 @@ def test_library_exports_every_header_symbol():
     from nanovllm_amd import _lib
 
     declared = _lib.exported_symbols_from_header(HEADER)
-    assert len(declared) == 20, declared
+    assert len(declared) == 22, declared
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
@@ -135,6 +135,76 @@ def test_mtp_and_attention_validation():
     st = _lib.lib.nvdsa_sparse_tail_attention(*[ctypes.byref(x) for x in a], 0.1, ctypes.byref(out), 0x2000,
                                               1 << 30, None)
     assert st == 1 and "power of two" in _lib.last_error()
+
+
+@pytest.mark.parametrize("mutate,code,msg", [
+    (lambda d: setattr(d[0], "ndim", 2), 1, "q_inout rank mismatch."),
+    (lambda d: setattr(d[1], "dtype", 1), 2, "cos dtype mismatch."),
+    (lambda d: setattr(d[2], "ndim", 3), 1, "sin rank mismatch."),
+    (lambda d: setattr(d[2], "contiguous", 0), 3, "sin must be contiguous."),
+    (lambda d: [setattr(x, "dtype", 3) for x in d], 2, "float16 or bfloat16"),
+    (lambda d: setattr(d[1], "device", 1), 4, "same GPU"),
+    (lambda d: d[0].shape.__setitem__(0, 0), 1, "non-empty"),
+    (lambda d: d[1].shape.__setitem__(0, 3), 1, "token dimension mismatch"),
+    (lambda d: d[0].shape.__setitem__(1, 160), 1, "n_head <= 128"),
+    (lambda d: d[0].shape.__setitem__(2, 264), 1, "head_dim <= 256"),
+])
+def test_query_rope_validation(mutate, code, msg):
+    """The reference adapter's checks (dsa_indexer_project_torch_adpt.h:42-90)."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd._lib import BFLOAT16
+
+    d = [_desc((4, 32, 128), BFLOAT16), _desc((4, 1, 1, 64), BFLOAT16), _desc((4, 1, 1, 64), BFLOAT16)]
+    mutate(d)
+    assert _lib.lib.nvdsa_dsa_indexer_query_rope_inplace(*[ctypes.byref(x) for x in d], 64, None) == code
+    assert msg in _lib.last_error()
+    d = [_desc((4, 32, 128), BFLOAT16), _desc((4, 1, 1, 256), BFLOAT16), _desc((4, 1, 1, 256), BFLOAT16)]
+    for rope, m in ((48 + 8, "aligned to 16"), (0, "positive"), (144, "no larger than head_dim")):
+        assert _lib.lib.nvdsa_dsa_indexer_query_rope_inplace(*[ctypes.byref(x) for x in d], rope, None) == 7
+        assert m in _lib.last_error()
+    d[1].shape[3] = d[2].shape[3] = 16  # the storage check comes first (adapter order)
+    assert _lib.lib.nvdsa_dsa_indexer_query_rope_inplace(*[ctypes.byref(x) for x in d], 64, None) == 1
+    assert "storage is smaller" in _lib.last_error()
+
+
+def test_indexer_project_validation():
+    from nanovllm_amd import _lib
+    from nanovllm_amd._lib import BFLOAT16, FLOAT32
+
+    T = 3
+
+    def descs():
+        return [_desc((T, 6144), BFLOAT16), _desc((T, 2048), BFLOAT16), _desc((T, 1, 1, 64), BFLOAT16),
+                _desc((T, 1, 1, 64), BFLOAT16), _desc((4096, 2048), BFLOAT16), _desc((32, 6144), BFLOAT16),
+                _desc((T, 32, 128), BFLOAT16), _desc((T, 32), BFLOAT16)]
+
+    def call(d, heads=32, hd=128, rope=64):
+        ptrs = [ctypes.byref(x) if x is not None else None for x in d]
+        return _lib.lib.nvdsa_dsa_indexer_project_query_only(*ptrs, heads, hd, rope, 1.0, None)
+
+    d = descs()
+    d[6].shape[1] = 16
+    assert call(d) == 1 and _lib.last_error().endswith("q_index_out shape must be (3, 32, 128), got (3, 16, 128)")
+    d = descs()
+    d[7].shape[1] = 64
+    assert call(d) == 1 and "index_weights_out shape must be (3, 32), got (3, 64)" in _lib.last_error()
+    d = descs()
+    d[5] = None
+    assert call(d) == 7 and "go together" in _lib.last_error()
+    d = descs()
+    d[1].shape[1] = d[4].shape[1] = 2000
+    assert call(d) == 1 and "multiple of 256" in _lib.last_error()
+    d = descs()
+    d[5].dtype = FLOAT32
+    assert call(d) == 2 and "one 16-bit dtype" in _lib.last_error()
+    d = descs()
+    d[2].shape[3] = d[3].shape[3] = 32
+    assert call(d) == 1 and "rope_dim values per token" in _lib.last_error()
+    d = descs()
+    assert call(d, rope=63) == 7 and "even" in _lib.last_error()
+    d = descs()
+    d[4].data = 0x1008
+    assert call(d) == 3 and "16-byte aligned" in _lib.last_error()
 
 
 def test_torch_library_schemas_match_reference():
