@@ -362,6 +362,7 @@ def main() -> int:
         rows["cfg2_bs64_mixed"] = measure_cfg2(torch, np, dev, args.seed)
         rows["lidu_init"] = measure_lidu_init(torch, np, dev, args.seed)
         rows["indexer_project"] = measure_indexer(torch, dev, args.seed)
+        rows["prefill_persist"] = measure_persist(torch, dev, args.seed)
 
     value_us = graph_ms * 1000.0
     line = {
@@ -678,6 +679,50 @@ def measure_indexer(torch, dev, seed: int, reps: int = 20):
             "hbm_GBs": round(algo / (k_us * 1e-6) / 1e9, 1),
             "frac_of_peak": round(algo / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
             "fused_call_us": round(fused_us, 2), "library_gemms_plus_rope_us": round(lib_us, 2)}
+
+
+def measure_persist(torch, dev, seed: int, reps: int = 5):
+    """Prefill -> DRAM persistence of one layer of a 65536-token prompt (512
+    full blocks, 144 KiB each, scattered block ids) in one launch, against a
+    pinned device -> host hipMemcpyAsync of 256 MiB."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd import ops
+    from nanovllm_amd.host_memory import empty_host_mapped
+
+    nb = 512
+    g = torch.Generator().manual_seed(seed)
+    hckv = torch.randn(nb + 64, 128, 1, 512, generator=g).to(torch.bfloat16).to(dev)
+    hkpe = torch.randn(nb + 64, 128, 1, 64, generator=g).to(torch.bfloat16).to(dev)
+    dckv = empty_host_mapped((nb + 64, 128, 1, 512), torch.bfloat16, dev)
+    dkpe = empty_host_mapped((nb + 64, 128, 1, 64), torch.bfloat16, dev)
+    hid = torch.randperm(nb + 64, generator=g)[:nb].to(torch.int32).to(dev)
+    did = torch.randperm(nb + 64, generator=g)[:nb].to(torch.int32).to(dev)
+    ops.persist_prefill_blocks(hckv, hkpe, dckv, dkpe, hid, did)
+    torch.cuda.synchronize()
+    with _lib.KernelTimer(capacity=2 * reps) as kt:
+        for _ in range(reps):
+            ops.persist_prefill_blocks(hckv, hkpe, dckv, dkpe, hid, did)
+        torch.cuda.synchronize()
+    us = kt.mean_ms("persist_blocks_kernel") * 1000.0
+    nbytes = nb * 128 * (512 + 64) * 2
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(3):
+        dst.copy_(src, non_blocking=True)
+    e.record()
+    e.synchronize()
+    d2h = 3 * n / (s.elapsed_time(e) * 1e6)
+    rate = nbytes / (us * 1e-6) / 1e9
+    del hckv, hkpe, dckv, dkpe, src, dst
+    torch.cuda.empty_cache()
+    return {"workload": f"{nb} full blocks (65536-token prompt), CKV+KPE {nbytes} bytes, HBM -> host-mapped DRAM",
+            "kernel_us": round(us, 1), "d2h_GBs": round(rate, 2), "measured_memcpy_d2h_GBs": round(d2h, 2),
+            "frac_of_measured": round(rate / d2h, 3)}
 
 
 def cpu_baseline(case, queries_cpu, steps: int):

@@ -4,8 +4,9 @@
  * Seven entry points replace the seven torch.library operators that the
  * reference registers under the `nanovllm_dsa` namespace
  * (reference: csrc/nanovllm_ascend_ops/bindings/nanovllm_ops.cpp:645-696);
- * further ones cover the first-decode initialisation and the decode
- * indexer projection that produces the LIM inputs.
+ * further ones cover the first-decode initialisation, the decode indexer
+ * projection that produces the LIM inputs and the prefill -> DRAM
+ * persistence of full KV blocks.
  * Each takes its arguments in the same order as the reference schema, as
  * plain tensor descriptors (device address + dtype + shape), plus the HIP
  * stream to launch on.  Every entry point:
@@ -321,6 +322,22 @@ int nvdsa_dsa_indexer_project_query_only(const nvdsa_tensor* hidden_states,
                                          int64_t rope_dim,
                                          double score_scale,
                                          void* stream);
+
+/* Prefill -> DRAM persistence of full KV blocks in one launch: for every i,
+ * dram_kv_cache[dram_block_ids[i]] = hbm_kv_cache[hbm_block_ids[i]] and the
+ * same for the rope caches.  Caches [blocks, 128, 512] / [blocks, 128, 64]
+ * (or with the reference's singleton third dim); the DRAM caches may be
+ * host-mapped (device NVDSA_HOST_MAPPED_DEVICE).  A pair whose ids do not
+ * name a block of the caches is skipped on the device.  Replaces the
+ * per-block synchronous copies of GlmMLAAttention.finalize_prefill_offload
+ * (reference nanovllm/models/glm_mla.py:883-889).  No workspace. */
+int nvdsa_persist_prefill_blocks(const nvdsa_tensor* hbm_kv_cache,
+                                 const nvdsa_tensor* hbm_k_rope,
+                                 const nvdsa_tensor* dram_kv_cache,
+                                 const nvdsa_tensor* dram_k_rope,
+                                 const nvdsa_tensor* hbm_block_ids,
+                                 const nvdsa_tensor* dram_block_ids,
+                                 void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Pinned, device-mapped host memory for the DRAM KV caches: the counterpart

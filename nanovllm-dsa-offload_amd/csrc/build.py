@@ -20,7 +20,7 @@ PKG_ROOT = CSRC.parent
 REPO = PKG_ROOT.parent
 BUILD_DIR = REPO / "_build" / "nvdsa"
 OUTPUT = PKG_ROOT / "nanovllm_amd" / "libnvdsa.so"
-SOURCES = ("scatter_copy.hip", "lim.hip", "sfa.hip", "indexer.hip", "nvdsa_abi.hip")
+SOURCES = ("scatter_copy.hip", "lim.hip", "sfa.hip", "indexer.hip", "persist.hip", "nvdsa_abi.hip")
 ARCH = os.environ.get("NVDSA_OFFLOAD_ARCH", "gfx950")
 
 COMMON_FLAGS = [

@@ -182,7 +182,7 @@ const char* nvdsa_kernel_name(int32_t kernel_id) {
                                 "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel",
                                 "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
                                 "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied", "indexer_project_kernel",
-                                "indexer_rope_kernel"};
+                                "indexer_rope_kernel", "persist_blocks_kernel"};
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }
@@ -1002,6 +1002,52 @@ int nvdsa_dsa_indexer_project_query_only(const nvdsa_tensor* hidden_states, cons
   a.elem = elem_of(hidden_states);
   return launch_status(nvdsa::launch_indexer_project(a, static_cast<hipStream_t>(stream)),
                        "dsa_indexer_project_query_only");
+}
+
+// ------------------------------------------------------------------------
+int nvdsa_persist_prefill_blocks(const nvdsa_tensor* hbm_kv_cache, const nvdsa_tensor* hbm_k_rope,
+                                 const nvdsa_tensor* dram_kv_cache, const nvdsa_tensor* dram_k_rope,
+                                 const nvdsa_tensor* hbm_block_ids, const nvdsa_tensor* dram_block_ids, void* stream) {
+  const nvdsa_tensor* const all[] = {hbm_kv_cache, hbm_k_rope, dram_kv_cache, dram_k_rope, hbm_block_ids,
+                                     dram_block_ids};
+  if (!all_nonnull(all)) return fail(NVDSA_ERR_ARG, "persist_prefill_blocks: null tensor argument");
+  Check c("persist_prefill_blocks");
+  auto cache_ok = [](const nvdsa_tensor* t, int64_t width) {
+    return (dims_are(t, 3) && sz(t, 1) == 128 && sz(t, 2) == width) ||
+           (dims_are(t, 4) && sz(t, 1) == 128 && sz(t, 2) == 1 && sz(t, 3) == width);
+  };
+  c.need(cache_ok(hbm_kv_cache, 512) && cache_ok(dram_kv_cache, 512), NVDSA_ERR_SHAPE,
+         "CKV caches must be [blocks, 128, (1,) 512]")
+      .need(cache_ok(hbm_k_rope, 64) && cache_ok(dram_k_rope, 64), NVDSA_ERR_SHAPE,
+            "KPE caches must be [blocks, 128, (1,) 64]")
+      .need(sz(hbm_kv_cache, 0) == sz(hbm_k_rope, 0) && sz(dram_kv_cache, 0) == sz(dram_k_rope, 0), NVDSA_ERR_SHAPE,
+            "CKV and KPE caches must hold the same number of blocks")
+      .need(dims_are(hbm_block_ids, 1) && same_shape(hbm_block_ids, dram_block_ids), NVDSA_ERR_SHAPE,
+            "block id lists must be rank one and of equal length")
+      .need(hbm_block_ids->dtype == NVDSA_INT32 && dram_block_ids->dtype == NVDSA_INT32, NVDSA_ERR_DTYPE,
+            "block ids must be int32")
+      .need(is_half(hbm_kv_cache) && hbm_k_rope->dtype == hbm_kv_cache->dtype &&
+                dram_kv_cache->dtype == hbm_kv_cache->dtype && dram_k_rope->dtype == hbm_kv_cache->dtype,
+            NVDSA_ERR_DTYPE, "caches must share one 16-bit dtype");
+  if (c.ok()) {
+    check_common(c, all, hbm_kv_cache->device, dram_kv_cache, dram_k_rope);
+    c.need(hbm_kv_cache->device >= 0, NVDSA_ERR_DEVICE, "HBM caches must be on a GPU")
+        .need(aligned16(hbm_kv_cache) && aligned16(hbm_k_rope) && aligned16(dram_kv_cache) && aligned16(dram_k_rope),
+              NVDSA_ERR_LAYOUT, "caches must be 16-byte aligned");
+  }
+  if (!c.ok()) return c.finish();
+  nvdsa::PersistArgs a{};
+  a.hbm_ckv = hbm_kv_cache->data;
+  a.hbm_kpe = hbm_k_rope->data;
+  a.dram_ckv = dram_kv_cache->data;
+  a.dram_kpe = dram_k_rope->data;
+  a.hbm_ids = static_cast<const int32_t*>(hbm_block_ids->data);
+  a.dram_ids = static_cast<const int32_t*>(dram_block_ids->data);
+  a.count = sz(hbm_block_ids, 0);
+  a.hbm_blocks = sz(hbm_kv_cache, 0);
+  a.dram_blocks = sz(dram_kv_cache, 0);
+  if (a.count * 4 >= kMaxGridThreads / 256) return fail(NVDSA_ERR_SHAPE, "persist_prefill_blocks: too many blocks");
+  return launch_status(nvdsa::launch_persist_blocks(a, static_cast<hipStream_t>(stream)), "persist_prefill_blocks");
 }
 
 // ------------------------------------------------------------------------

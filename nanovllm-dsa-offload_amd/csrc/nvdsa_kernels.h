@@ -29,7 +29,8 @@ enum KernelId : int {
   kKernSfaSplitCopied = 13,
   kKernIdxProject = 14,
   kKernIdxRope = 15,
-  kKernCount = 16
+  kKernPersist = 16,
+  kKernCount = 17
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.
@@ -201,5 +202,17 @@ struct RopeArgs {
   Elem elem;
 };
 hipError_t launch_indexer_rope(const RopeArgs& a, hipStream_t stream);
+
+// ---- prefill -> DRAM persistence ------------------------------------------
+struct PersistArgs {
+  const void* hbm_ckv;      // [hbm_blocks, 128, 512]
+  const void* hbm_kpe;      // [hbm_blocks, 128, 64]
+  void* dram_ckv;           // [dram_blocks, 128, 512] (host-mapped)
+  void* dram_kpe;           // [dram_blocks, 128, 64]
+  const int32_t* hbm_ids;   // [count]
+  const int32_t* dram_ids;  // [count]
+  int64_t count, hbm_blocks, dram_blocks;
+};
+hipError_t launch_persist_blocks(const PersistArgs& a, hipStream_t stream);
 
 }  // namespace nvdsa

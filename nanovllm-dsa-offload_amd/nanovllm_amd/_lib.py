@@ -71,6 +71,7 @@ SIGNATURES = {
     "nvdsa_initialize_lidu_row_shared": ([_P, _I64] + [_P] * 6 + [_VP, _SZ, _VP], ctypes.c_int),
     "nvdsa_dsa_indexer_query_rope_inplace": ([_P] * 3 + [_I64, _VP], ctypes.c_int),
     "nvdsa_dsa_indexer_project_query_only": ([_P] * 8 + [_I64, _I64, _I64, _DBL, _VP], ctypes.c_int),
+    "nvdsa_persist_prefill_blocks": ([_P] * 6 + [_VP], ctypes.c_int),
     "nvdsa_host_mapped_alloc": ([_SZ, ctypes.POINTER(_VP), ctypes.POINTER(_VP)], ctypes.c_int),
     "nvdsa_host_mapped_free": ([_VP], ctypes.c_int),
     "nvdsa_profile_begin": ([ctypes.c_int32], ctypes.c_int),

@@ -268,6 +268,13 @@ def indexer_project_query_only(hidden_states, q_c, cos, sin, wq_b_weight, weight
         int(n_head), int(head_dim), int(rope_dim), float(score_scale), _stream_of(q_c)))
 
 
+def persist_prefill_blocks(hbm_kv_cache, hbm_k_rope, dram_kv_cache, dram_k_rope, hbm_block_ids,
+                           dram_block_ids) -> None:
+    """nvdsa_persist_prefill_blocks on the current stream (no host sync)."""
+    descs = [_D(t) for t in (hbm_kv_cache, hbm_k_rope, dram_kv_cache, dram_k_rope, hbm_block_ids, dram_block_ids)]
+    _lib.check(_L.nvdsa_persist_prefill_blocks(*map(_ref, descs), _stream_of(hbm_kv_cache)))
+
+
 IMPLS = {
     "fused_li_manage": _fused_li_manage,
     "fused_li_manage_mtp": _fused_li_manage_mtp,

@@ -24,7 +24,9 @@ It restates, in numpy, the semantics of the seven reference operators:
 * ``fused_copy_sfa(_mtp)`` — the composition scatter_copy -> attention
   (ut_ops/test_fused_copy_sfa.py:453-497, README_ops.md:99-141);
 * ``initialize_lidu_row(_shared)`` — the first-decode top-C initialisation
-  and its IndexShare copy (nanovllm/models/dsa_offload_ops.py:251-411).
+  and its IndexShare copy (nanovllm/models/dsa_offload_ops.py:251-411);
+* ``persist_blocks`` / ``finalize_prefill_pool_row`` — the prefill -> DRAM
+  hand-over of one layer (nanovllm/models/glm_mla.py:850-891).
 
 Where the reference leaves a choice implementation-defined (victim choice —
 a hash-seeded partial scan in fused_li_manage_service_vector.h:72-81,
@@ -332,6 +334,33 @@ def resolve_row(token: int, table_row: np.ndarray, num_blocks: int) -> int:
     if blk < 0 or blk >= num_blocks:
         return -1
     return blk * BLOCK + (token & (BLOCK - 1))
+
+
+def persist_blocks(hbm_ckv, hbm_kpe, dram_ckv, dram_kpe, hbm_ids, dram_ids) -> None:
+    """Prefill -> DRAM persistence (nanovllm/models/glm_mla.py:883-889):
+    dram_*[dram_ids[i]] = hbm_*[hbm_ids[i]] for every i, CKV and KPE; a pair
+    whose ids name no block of the caches is skipped (the reference would
+    index with them; the ABI keeps the device from faulting).  Mutates the
+    DRAM arrays ([blocks, 128, ...] of any trailing shape)."""
+    for h, d in zip(np.asarray(hbm_ids).tolist(), np.asarray(dram_ids).tolist()):
+        if 0 <= h < hbm_ckv.shape[0] and 0 <= d < dram_ckv.shape[0]:
+            dram_ckv[d] = hbm_ckv[h]
+            dram_kpe[d] = hbm_kpe[h]
+
+
+def finalize_prefill_pool_row(row, num_full_blocks: int, num_sparse_blocks: int, cache_tokens: int,
+                              owner: bool = True, block: int = BLOCK) -> bool:
+    """The pool-row part of finalize_prefill_offload (glm_mla.py:857-880): the
+    owner resets the row to -1; a short request (num_sparse >= num_full)
+    maps token t to slot t for t < num_full*block when the budget is
+    nonzero.  Returns True when the blocks must be persisted to DRAM."""
+    if owner:
+        row[:] = -1
+    if num_sparse_blocks >= num_full_blocks:
+        if owner and cache_tokens > 0 and num_full_blocks > 0:
+            row[:num_full_blocks * block] = np.arange(num_full_blocks * block)
+        return False
+    return True
 
 
 def scatter_copy(src_ids, dst_slots, copy_counts, hbm_table, dram_table, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv):

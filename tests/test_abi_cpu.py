@@ -20,7 +20,7 @@ def test_library_exports_every_header_symbol():
     from nanovllm_amd import _lib
 
     declared = _lib.exported_symbols_from_header(HEADER)
-    assert len(declared) == 22, declared
+    assert len(declared) == 23, declared
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
@@ -205,6 +205,41 @@ def test_indexer_project_validation():
     d = descs()
     d[4].data = 0x1008
     assert call(d) == 3 and "16-byte aligned" in _lib.last_error()
+
+
+def test_persist_validation():
+    from nanovllm_amd import _lib
+    from nanovllm_amd._lib import BFLOAT16, FLOAT16, INT32
+
+    def descs():
+        return [_desc((8, 128, 512), BFLOAT16), _desc((8, 128, 64), BFLOAT16),
+                _desc((16, 128, 1, 512), BFLOAT16, device=-1), _desc((16, 128, 1, 64), BFLOAT16, device=-1),
+                _desc((5,), INT32), _desc((5,), INT32)]
+
+    def call(d):
+        return _lib.lib.nvdsa_persist_prefill_blocks(*[ctypes.byref(x) for x in d], None)
+
+    d = descs()
+    d[0].shape[2] = 256
+    assert call(d) == 1 and "CKV caches" in _lib.last_error()
+    d = descs()
+    d[3].shape[0] = 15
+    assert call(d) == 1 and "same number of blocks" in _lib.last_error()
+    d = descs()
+    d[5].shape[0] = 4
+    assert call(d) == 1 and "equal length" in _lib.last_error()
+    d = descs()
+    d[4].dtype = BFLOAT16
+    assert call(d) == 2 and "int32" in _lib.last_error()
+    d = descs()
+    d[2].dtype = d[3].dtype = FLOAT16
+    assert call(d) == 2 and "one 16-bit dtype" in _lib.last_error()
+    d = descs()
+    d[0].device = -1
+    assert call(d) == 4
+    d = descs()
+    d[1].data = 0x1004
+    assert call(d) == 3 and "aligned" in _lib.last_error()
 
 
 def test_torch_library_schemas_match_reference():

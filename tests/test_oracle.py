@@ -462,3 +462,45 @@ def test_attention_mtp_causal_visible_length():
     out2 = O.sparse_tail_attention(**a2, scale=1 / 24, rows_per_request=4)
     assert np.allclose(out2[0], out[0])
     assert not np.allclose(out2[3], out[3])
+
+
+# --------------------------------------------------------------------------
+# prefill -> DRAM hand-over
+def test_persist_blocks_brute_force():
+    rng = np.random.default_rng(11)
+    hbm_ckv = rng.integers(0, 1 << 16, (5, 128, 1, 8), dtype=np.uint16)
+    hbm_kpe = rng.integers(0, 1 << 16, (5, 128, 1, 2), dtype=np.uint16)
+    dram_ckv = rng.integers(0, 1 << 16, (7, 128, 1, 8), dtype=np.uint16)
+    dram_kpe = rng.integers(0, 1 << 16, (7, 128, 1, 2), dtype=np.uint16)
+    before_c, before_k = dram_ckv.copy(), dram_kpe.copy()
+    hbm_ids = np.array([4, 0, -1, 2, 9], np.int32)
+    dram_ids = np.array([1, 6, 3, 7, 2], np.int32)  # pairs 3 (dram 7) and 4 (hbm 9) and 2 (hbm -1) are skipped
+    O.persist_blocks(hbm_ckv, hbm_kpe, dram_ckv, dram_kpe, hbm_ids, dram_ids)
+    for d in range(7):
+        for t in range(128):
+            for e in range(8):
+                want = {1: hbm_ckv[4], 6: hbm_ckv[0]}.get(d, before_c[d])[t, 0, e]
+                assert dram_ckv[d, t, 0, e] == want
+            for e in range(2):
+                want = {1: hbm_kpe[4], 6: hbm_kpe[0]}.get(d, before_k[d])[t, 0, e]
+                assert dram_kpe[d, t, 0, e] == want
+
+
+def test_finalize_prefill_pool_row_branches():
+    row = np.full(1024, 7, np.int32)
+    # long request: reset only, persist
+    assert O.finalize_prefill_pool_row(row, num_full_blocks=5, num_sparse_blocks=2, cache_tokens=2048)
+    assert (row == -1).all()
+    # short request with a budget: identity over the full blocks
+    row[:] = 7
+    assert not O.finalize_prefill_pool_row(row, num_full_blocks=3, num_sparse_blocks=3, cache_tokens=2048)
+    assert np.array_equal(row[:384], np.arange(384)) and (row[384:] == -1).all()
+    # short request, no budget: reset only
+    row[:] = 7
+    assert not O.finalize_prefill_pool_row(row, num_full_blocks=3, num_sparse_blocks=4, cache_tokens=0)
+    assert (row == -1).all()
+    # shared (non-owner) layer: the row is not touched
+    row[:] = 7
+    assert O.finalize_prefill_pool_row(row, num_full_blocks=5, num_sparse_blocks=2, cache_tokens=2048, owner=False)
+    assert (row == 7).all()
+
