@@ -910,7 +910,9 @@ __device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int 
   const int tid = threadIdx.x;
   int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
   int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
-  const int nv = select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
+  // Budgets up to 2048 slots: slot states and keys in registers, 4 per thread.
+  const int nv = c <= 4 * kManageThreads ? select_victims_regs<4>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
+                                         : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
   // Misses first (ascending token), paired with ascending victim slots.
   for (int i = tid; i < m; i += kManageThreads) {
     const int t = misses[i];
