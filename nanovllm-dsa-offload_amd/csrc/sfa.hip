@@ -576,7 +576,7 @@ __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials pa
   *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
 }
 
-constexpr int kCombineMaxS = 8;
+constexpr int kCombineMaxS = 16;
 
 template <typename T>
 void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int splits, hipStream_t stream) {
