@@ -62,7 +62,8 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-rows", action="store_true",
-                   help="skip the per-row measurements at BASELINE configs[2], configs[3] and the LIDU init")
+                   help="skip the per-row measurements (BASELINE configs[2]-[4], LIDU init, indexer "
+                        "projection, prefill persist)")
     p.add_argument("--cpu-steps", type=int, default=8, help="layer-steps of the CPU oracle sample")
     p.add_argument("--kernels-only", choices=("lim", "fused", "split", "sfa", "copy"), default=None,
                    help="launch one kernel family alone (for rocprofv3 --pmc) and exit")
@@ -387,6 +388,7 @@ def main() -> int:
                          "combine_us": round(k["sfa_combine_kernel"] * 1000, 2)}}
         rows["cfg3_mtp3"] = measure_mtp3(torch, np, dev, args.seed)
         rows["cfg2_bs64_mixed"] = measure_cfg2(torch, np, dev, args.seed)
+        rows["cfg4_indexshare"] = measure_cfg4(torch, np, dev, args.seed)
         rows["lidu_init"] = measure_lidu_init(torch, np, dev, args.seed)
         rows["indexer_project"] = measure_indexer(torch, dev, args.seed)
         rows["prefill_persist"] = measure_persist(torch, dev, args.seed)
@@ -602,6 +604,96 @@ def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
                                       / 1e9, 1),
            "fused_h2d_GBs": round(miss_rows * ROW_BYTES / (km["sfa_split_kernel_fused"] * 1e-6) / 1e9, 2)}
     del d, t, case
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
+    """the IndexShare full decode step.  78 layers on the
+    GLM-5.2 schedule (21 owners run LIM, 57 shared layers reuse their owner's
+    selection), bs=8, 65536-token prompts, C=2048, misses 5-15% (alternating
+    calibrated queries), offload_fuse.  Every layer has its own HBM caches and
+    its own pinned host-mapped DRAM caches (77 x 604 MB beside layer 0's);
+    every owner its own index keys and pool.  The whole 78-layer step is one
+    HIP graph (two, for the two query parities, replayed in turn)."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd.host_memory import empty_host_mapped
+    from nanovllm_amd.index_share import (CONTEXT_FIELDS, DsaLayerCaches, IndexShareDecodeStep,
+                                          IndexShareGroupManager, glm52_indexer_types)
+    from nanovllm_amd.workloads import make_drift_case
+
+    L, B, N, C = 78, 8, 65536, 2048
+    rng = np.random.default_rng(1004)
+    tails = rng.integers(1, 128, size=B)
+    t0 = time.time()
+    case = make_drift_case(B, N, C, tails, seed=seed, calib_device=dev)
+    d = case.to_device(dev)
+    t = d.tensors
+    groups = IndexShareGroupManager(L, glm52_indexer_types(L))
+    layers = []
+    for i in range(L):
+        if i == 0:
+            caches = [t[n] for n in ("hbm_k_rope", "hbm_kv_cache", "dram_k_rope", "dram_kv_cache")]
+        else:
+            caches = [t["hbm_k_rope"].clone(), t["hbm_kv_cache"].clone()]
+            for n in ("dram_k_rope", "dram_kv_cache"):
+                dram = empty_host_mapped(t[n].shape, t[n].dtype, dev)
+                dram.copy_(t[n])
+                caches.append(dram)
+        own = {}
+        if groups.is_owner(i):
+            own = dict(index_key_cache=t["index_key_cache"] if i == 0 else t["index_key_cache"].clone(),
+                       cache_slots_pool=t["cache_slots_pool"] if i == 0 else t["cache_slots_pool"].clone())
+        layers.append(DsaLayerCaches(*caches, **own))
+    torch.cuda.synchronize()
+    dram_bytes = L * sum(t[n].numel() * 2 for n in ("dram_k_rope", "dram_kv_cache"))
+    log(f"bench: built cfg4 case ({L} layers, {dram_bytes / 1e9:.1f} GB of host-mapped DRAM) in "
+        f"{time.time() - t0:.1f}s")
+    runner = IndexShareDecodeStep(groups, layers)
+    ctx = {f: t[f] for f in CONTEXT_FIELDS}
+    qs = [t["query_index_b"], t["query_index"]]
+    base = dict(query_rope=t["query_rope"], query=t["query"], scale=case.meta["scale"],
+                attention_out=t["attention_out"])
+
+    def step(i):
+        owner_kw = dict(base, query_index=qs[i % 2], index_weights=t["index_weights"])
+        runner.step(ctx, lambda layer: owner_kw if groups.is_owner(layer) else base)
+
+    for i in range(2):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / steps
+    misses = []
+    with _lib.KernelTimer(capacity=256 * steps) as kt:
+        for i in range(steps):
+            step(i)
+            misses.append(int(runner.owner_outputs(0, B)["miss_counts"].sum()))
+    torch.cuda.synchronize()
+    names = ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel")
+    km = _kernel_means(kt, names)
+    per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names}
+    graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran
+    miss_rows = float(np.mean(misses))  # per layer (every member copies its owner's misses)
+    n_tokens = int(t["num_candidate_tokens"].sum())
+    copy_bytes = L * miss_rows * ROW_BYTES
+    out = {"workload": f"{L} layers (GLM-5.2 IndexShare: {groups.num_groups} owners run LIM, "
+                       f"{len(groups.shared_layer_idxs)} shared), bs={B}, prompts {N}, C={C}, tails U[1,127], "
+                       "misses 5-15%, offload_fuse, one HIP graph per step",
+           "step_ms": round(graph_ms, 3), "eager_step_ms": round(eager_ms, 3),
+           "us_per_layer": round(graph_ms * 1000 / L, 2),
+           "miss_rows_per_layer": round(miss_rows, 1), "host_link_bytes_per_step": int(copy_bytes),
+           "kernels_us": km, "kernels_us_per_step": per_step,
+           "lim_score_hbm_GBs": round((n_tokens * KEY_ROW_BYTES + 4 * n_tokens) / (km["lim_score_kernel"] * 1e-6)
+                                      / 1e9, 1),
+           "fused_h2d_GBs": round(miss_rows * ROW_BYTES / (km["sfa_split_kernel_fused"] * 1e-6) / 1e9, 2),
+           "step_h2d_GBs": round(copy_bytes / (graph_ms * 1e-3) / 1e9, 2)}
+    del runner, layers, d, t, case
     torch.cuda.empty_cache()
     return out
 

@@ -504,71 +504,73 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_mtp_overlap_kernel(SfaArgs a
   sfa_split_body<T, false, kKeysResident>(a, part, splits, 0, splits_total, i % attn_blocks, i / attn_blocks);
 }
 
-// Merge split partials: one 128-thread workgroup per (row, head), 4 dims per
-// thread.  MAXS > 0 (splits <= MAXS): every split's (m, l) and output slice
-// are loaded at once -- an index past the last split rereads the last one
-// and is ignored -- so the merge waits on one round of loads instead of two
-// dependent ones.  MAXS == 0 loops over any number of splits.  Both sum in
-// split order, so they round identically.
-template <typename T, int MAXS>
+// Merge split partials: one 128-thread workgroup per (row, head), 4 of the
+// 512 latent dims per thread.  Lane s of each wave reads split s's (m, l)
+// (and split s + 64's), so the running max, the weights exp2(m_s - max) and
+// the softmax denominator come from one load and two wave reductions.  The
+// output slices are loaded kCombineBatch splits at a time, all in flight
+// together (the first batch is issued before the reductions), and summed in
+// split order.  Splits with l == 0 hold no keys and are skipped.  A small
+// batch launches many splits per row (e.g. 32 at 8 rows), which a chain of
+// one dependent load per split would turn into a latency-bound merge.
+constexpr int kCombineBatch = 16;
+constexpr int kCombineMaxSplits = 2 * kWave;
+static_assert(2 * kMaxSplits <= kCombineMaxSplits, "an MTP3 launch pair merges up to 2 x kMaxSplits splits");
+
+template <typename T>
 __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
-  const int64_t row = blockIdx.x;
-  const int head = blockIdx.y;
   const int64_t H = a.heads;
-  float mmax = -INFINITY;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float total = 0.f;
-  if constexpr (MAXS > 0) {
-    float2 ml[MAXS];
-    float4 o[MAXS];
+  const int lane = threadIdx.x & (kWave - 1);
+  // The partial of (row, split s, head) sits at index base + s * H.
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * splits * H + blockIdx.y;
+  const float2* mlp = reinterpret_cast<const float2*>(part.ml);
+  const float4* op = reinterpret_cast<const float4*>(part.o);
+  constexpr int kVec = kCkvDim / 4;
+  float2 v0 = make_float2(0.f, 0.f), v1 = v0;
+  if (lane < splits) v0 = mlp[base + lane * H];
+  if (lane + kWave < splits) v1 = mlp[base + (lane + kWave) * H];
+  float4 x[kCombineBatch];
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s) {
-      const int64_t pidx = (row * splits + (s < splits ? s : splits - 1)) * H + head;
-      ml[s] = reinterpret_cast<const float2*>(part.ml)[pidx];
-      o[s] = reinterpret_cast<const float4*>(part.o + pidx * kCkvDim)[threadIdx.x];
+  for (int j = 0; j < kCombineBatch; ++j)  // an index past the last split rereads it (ignored below)
+    x[j] = op[(base + min(j, splits - 1) * H) * kVec + threadIdx.x];
+  const bool live0 = v0.y > 0.f, live1 = v1.y > 0.f;
+  float m = fmaxf(live0 ? v0.x : -INFINITY, live1 ? v1.x : -INFINITY);
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  float w0 = 0.f, w1 = 0.f;
+  if (m != -INFINITY) {
+    w0 = live0 ? exp2f(v0.x - m) : 0.f;
+    w1 = live1 ? exp2f(v1.x - m) : 0.f;
+  }
+  float total = (live0 ? v0.y * w0 : 0.f) + (live1 ? v1.y * w1 : 0.f);
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) total += __shfl_xor(total, off, kWave);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < splits; s0 += kCombineBatch) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < kCombineBatch; ++j)
+        x[j] = op[(base + min(s0 + j, splits - 1) * H) * kVec + threadIdx.x];
     }
     // Consumed here, unconditionally: otherwise the compiler sinks each
-    // split's loads into its conditional use below, one wait each.
+    // split's load into its conditional use below, one wait each.
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s)
-      asm volatile("" : "+v"(ml[s].x), "+v"(ml[s].y), "+v"(o[s].x), "+v"(o[s].y), "+v"(o[s].z), "+v"(o[s].w));
+    for (int j = 0; j < kCombineBatch; ++j) asm volatile("" : "+v"(x[j].x), "+v"(x[j].y), "+v"(x[j].z), "+v"(x[j].w));
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s)
-      if (s < splits && ml[s].y > 0.f) mmax = fmaxf(mmax, ml[s].x);
-    if (mmax != -INFINITY) {
-#pragma unroll
-      for (int s = 0; s < MAXS; ++s) {
-        if (!(s < splits && ml[s].y > 0.f)) continue;
-        const float w = exp2f(ml[s].x - mmax);
-        total += ml[s].y * w;
-        acc.x += o[s].x * w;
-        acc.y += o[s].y * w;
-        acc.z += o[s].z * w;
-        acc.w += o[s].w * w;
-      }
-    }
-  } else {
-    for (int s = 0; s < splits; ++s) {
-      const int64_t pidx = (row * splits + s) * H + head;
-      if (part.ml[pidx * 2 + 1] > 0.f) mmax = fmaxf(mmax, part.ml[pidx * 2]);
-    }
-    if (mmax != -INFINITY) {
-      for (int s = 0; s < splits; ++s) {
-        const int64_t pidx = (row * splits + s) * H + head;
-        const float l = part.ml[pidx * 2 + 1];
-        if (!(l > 0.f)) continue;
-        const float w = exp2f(part.ml[pidx * 2] - mmax);
-        total += l * w;
-        const float4 o = reinterpret_cast<const float4*>(part.o + pidx * kCkvDim)[threadIdx.x];
-        acc.x += o.x * w;
-        acc.y += o.y * w;
-        acc.z += o.z * w;
-        acc.w += o.w * w;
+    for (int j = 0; j < kCombineBatch; ++j) {
+      const int s = s0 + j;  // uniform
+      const float ws = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s < kWave ? w0 : w1), s & (kWave - 1)));
+      if (s < splits && ws != 0.f) {
+        acc.x += x[j].x * ws;
+        acc.y += x[j].y * ws;
+        acc.z += x[j].z * ws;
+        acc.w += x[j].w * ws;
       }
     }
   }
   const float inv = total > 0.f ? 1.f / total : 0.f;
-  uint16_t* out = static_cast<uint16_t*>(a.out) + (row * H + head) * kCkvDim + threadIdx.x * 4;
+  uint16_t* out = static_cast<uint16_t*>(a.out) + (blockIdx.x * H + blockIdx.y) * kCkvDim + threadIdx.x * 4;
   const uint32_t lo = static_cast<uint32_t>(T::from_float(acc.x * inv)) |
                       (static_cast<uint32_t>(T::from_float(acc.y * inv)) << 16);
   const uint32_t hi = static_cast<uint32_t>(T::from_float(acc.z * inv)) |
@@ -576,15 +578,10 @@ __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials pa
   *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
 }
 
-constexpr int kCombineMaxS = 16;
-
 template <typename T>
 void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int splits, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads));
-  if (splits <= kCombineMaxS)
-    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, kCombineMaxS>, grid, dim3(128), stream, a, p, splits);
-  else
-    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, 0>, grid, dim3(128), stream, a, p, splits);
+  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>, grid, dim3(128), stream, a, p, splits);
 }
 
 template <typename T, bool FUSED>
