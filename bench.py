@@ -615,7 +615,10 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
     calibrated queries), offload_fuse.  Every layer has its own HBM caches and
     its own pinned host-mapped DRAM caches (77 x 604 MB beside layer 0's);
     every owner its own index keys and pool.  The whole 78-layer step is one
-    HIP graph (two, for the two query parities, replayed in turn)."""
+    HIP graph (two, for the two query parities, replayed in turn).  Also
+    timed: the group-prefetch mode (split path; each group's copies on a side
+    stream as soon as its owner has selected, every member's attention
+    waiting only for its own copy)."""
     from nanovllm_amd import _lib
     from nanovllm_amd.host_memory import empty_host_mapped
     from nanovllm_amd.index_share import (CONTEXT_FIELDS, DsaLayerCaches, IndexShareDecodeStep,
@@ -675,10 +678,29 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
             step(i)
             misses.append(int(runner.owner_outputs(0, B)["miss_counts"].sum()))
     torch.cuda.synchronize()
-    names = ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel")
+    names = ("lim_score_kernel", "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel_fused",
+             "sfa_combine_kernel")
     km = _kernel_means(kt, names)
     per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names}
     graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran
+    # Group prefetch: the split path with each group's copies on a side stream
+    # once its owner has selected (an even number of steps ran: parity 0).
+    pf = IndexShareDecodeStep(groups, layers, fused=False, prefetch=True)
+
+    def step_pf(i):
+        owner_kw = dict(base, query_index=qs[i % 2], index_weights=t["index_weights"])
+        pf.step(ctx, lambda layer: owner_kw if groups.is_owner(layer) else base)
+
+    for i in range(2):
+        step_pf(i)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(steps):
+        step_pf(i)
+    e1.record()
+    torch.cuda.synchronize()
+    pf_eager_ms = e0.elapsed_time(e1) / steps
+    pf_graph_ms = _graph_step_us(torch, [lambda: step_pf(0), lambda: step_pf(1)], steps) / 1000
     miss_rows = float(np.mean(misses))  # per layer (every member copies its owner's misses)
     n_tokens = int(t["num_candidate_tokens"].sum())
     copy_bytes = L * miss_rows * ROW_BYTES
@@ -686,14 +708,16 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
                        f"{len(groups.shared_layer_idxs)} shared), bs={B}, prompts {N}, C={C}, tails U[1,127], "
                        "misses 5-15%, offload_fuse, one HIP graph per step",
            "step_ms": round(graph_ms, 3), "eager_step_ms": round(eager_ms, 3),
+           "prefetch_step_ms": round(pf_graph_ms, 3), "prefetch_eager_step_ms": round(pf_eager_ms, 3),
            "us_per_layer": round(graph_ms * 1000 / L, 2),
            "miss_rows_per_layer": round(miss_rows, 1), "host_link_bytes_per_step": int(copy_bytes),
            "kernels_us": km, "kernels_us_per_step": per_step,
            "lim_score_hbm_GBs": round((n_tokens * KEY_ROW_BYTES + 4 * n_tokens) / (km["lim_score_kernel"] * 1e-6)
                                       / 1e9, 1),
            "fused_h2d_GBs": round(miss_rows * ROW_BYTES / (km["sfa_split_kernel_fused"] * 1e-6) / 1e9, 2),
-           "step_h2d_GBs": round(copy_bytes / (graph_ms * 1e-3) / 1e9, 2)}
-    del runner, layers, d, t, case
+           "step_h2d_GBs": round(copy_bytes / (graph_ms * 1e-3) / 1e9, 2),
+           "prefetch_step_h2d_GBs": round(copy_bytes / (pf_graph_ms * 1e-3) / 1e9, 2)}
+    del runner, pf, layers, d, t, case
     torch.cuda.empty_cache()
     return out
 

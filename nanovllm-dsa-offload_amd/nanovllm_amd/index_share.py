@@ -18,7 +18,9 @@ HBM cache.
   (or ``scatter_copy`` + ``sparse_tail_attention(_mtp)``) on its own caches
   with those buffers (reference glm_mla.py:1336-1406, :1542-1611,
   :1752-1881).  A shared layer that runs before its owner in a step raises,
-  as the reference does.
+  as the reference does.  With ``prefetch=True`` (split path) the copies of
+  a whole group run on a side stream as soon as its owner has selected, and
+  each member's attention waits only for its own copy.
 
 Nothing here allocates inside a step: the owner buffers are made once per
 batch size, so a step can be captured in one HIP graph.
@@ -152,13 +154,19 @@ class IndexShareDecodeStep:
     """Decode of one step over every layer of an IndexShare stack."""
 
     def __init__(self, groups: IndexShareGroupManager, layers: Sequence[DsaLayerCaches], *, mtp: bool = False,
-                 fused: bool = True) -> None:
+                 fused: bool = True, prefetch: bool = False) -> None:
         if len(layers) != groups.num_hidden_layers:
             raise ValueError(f"expected {groups.num_hidden_layers} layers, got {len(layers)}")
         for owner in groups.owner_layer_idxs:
             if layers[owner].index_key_cache is None or layers[owner].cache_slots_pool is None:
                 raise ValueError(f"owner layer {owner} needs index_key_cache and cache_slots_pool")
+        if prefetch and fused:
+            raise ValueError("prefetch copies on a side stream and attends with sparse_tail_attention: "
+                             "pass fused=False")
         self.groups, self.layers, self.mtp, self.fused = groups, list(layers), bool(mtp), bool(fused)
+        self.prefetch = bool(prefetch)
+        self._copy_stream: torch.cuda.Stream | None = None
+        self._events: list[torch.cuda.Event] = []
         self._outputs: dict[tuple[int, int], dict[str, torch.Tensor]] = {}
         self._selected: dict[int, int] = {}  # owner -> step id of its last selection
         self._step_id = 0
@@ -190,26 +198,51 @@ class IndexShareDecodeStep:
         self.groups.validate_layer(layer_idx)
         B = int(ctx["num_candidate_tokens"].shape[0])
         owner = self.groups.owner_of(layer_idx)
-        out = self.owner_outputs(owner, B)
         if layer_idx == owner:
-            if query_index is None or index_weights is None:
-                raise RuntimeError("LIDU decode requires indexer outputs.")
-            lay = self.layers[owner]
-            args = (query_index, index_weights, lay.index_key_cache, ctx["index_block_table"],
-                    ctx["num_candidate_tokens"], ctx["num_cache_tokens"], ctx["req_pool_entries"],
-                    lay.cache_slots_pool, out["topk_src_ids"], out["topk_dst_slots"])
-            if self.mtp:
-                ops.fused_li_manage_mtp(*args, out["miss_src_ids"], out["miss_dst_slots"], out["miss_counts"])
-            else:
-                ops.fused_li_manage(*args, out["miss_counts"])
-            self._selected[owner] = self._step_id
+            self._select(owner, ctx, B, query_index, index_weights)
         elif self._selected.get(owner) != self._step_id:
             raise RuntimeError(f"Shared layer {layer_idx} decode ran before its owner's LIM update "
                                f"(owner {owner}, batch_size={B}).")
+        if self.fused:
+            self._attend(layer_idx, ctx, B, query_rope, query, scale, attention_out, fused=True)
+        else:
+            self._copy(layer_idx, ctx, B)
+            self._attend(layer_idx, ctx, B, query_rope, query, scale, attention_out, fused=False)
+
+    def _select(self, owner: int, ctx, B: int, query_index, index_weights) -> None:
+        if query_index is None or index_weights is None:
+            raise RuntimeError("LIDU decode requires indexer outputs.")
+        out = self.owner_outputs(owner, B)
+        lay = self.layers[owner]
+        args = (query_index, index_weights, lay.index_key_cache, ctx["index_block_table"],
+                ctx["num_candidate_tokens"], ctx["num_cache_tokens"], ctx["req_pool_entries"],
+                lay.cache_slots_pool, out["topk_src_ids"], out["topk_dst_slots"])
+        if self.mtp:
+            ops.fused_li_manage_mtp(*args, out["miss_src_ids"], out["miss_dst_slots"], out["miss_counts"])
+        else:
+            ops.fused_li_manage(*args, out["miss_counts"])
+        self._selected[owner] = self._step_id
+
+    def _copy(self, layer_idx: int, ctx, B: int) -> None:
+        """The owner's misses, this layer's DRAM -> this layer's HBM.  The copy
+        takes 3-D cache views (reference glm_mla.py:1360-1363)."""
+        out = self.owner_outputs(self.groups.owner_of(layer_idx), B)
+        lay = self.layers[layer_idx]
+        views = (lay.hbm_k_rope.squeeze(2), lay.hbm_kv_cache.squeeze(2), lay.dram_k_rope.squeeze(2),
+                 lay.dram_kv_cache.squeeze(2))
+        if self.mtp:
+            ops.scatter_copy(out["miss_src_ids"], out["miss_dst_slots"], out["miss_counts"], ctx["hbm_block_table"],
+                             ctx["dram_block_table"], *views)
+        else:
+            ops.scatter_copy(out["topk_src_ids"].view(B, TOPK), out["topk_dst_slots"].view(B, TOPK),
+                             out["miss_counts"], ctx["hbm_block_table"], ctx["dram_block_table"], *views)
+
+    def _attend(self, layer_idx: int, ctx, B: int, query_rope, query, scale, attention_out, *, fused: bool) -> None:
+        out = self.owner_outputs(self.groups.owner_of(layer_idx), B)
         lay = self.layers[layer_idx]
         common = (query_rope, query, ctx["actual_seq_lengths_query"], ctx["actual_seq_lengths_kv"],
                   ctx["num_cache_tokens"], out["topk_dst_slots"])
-        if self.fused:
+        if fused:
             tail = (ctx["hbm_block_table"], ctx["dram_block_table"], lay.hbm_k_rope, lay.hbm_kv_cache,
                     lay.dram_k_rope, lay.dram_kv_cache, scale, attention_out)
             if self.mtp:
@@ -218,17 +251,7 @@ class IndexShareDecodeStep:
             else:
                 ops.fused_copy_sfa(*common, out["topk_src_ids"].view(B, TOPK), out["miss_counts"], *tail)
             return
-        # Split path: the copy takes 3-D cache views (reference glm_mla.py:1360-1363).
-        views = (lay.hbm_k_rope.squeeze(2), lay.hbm_kv_cache.squeeze(2), lay.dram_k_rope.squeeze(2),
-                 lay.dram_kv_cache.squeeze(2))
-        if self.mtp:
-            ops.scatter_copy(out["miss_src_ids"], out["miss_dst_slots"], out["miss_counts"], ctx["hbm_block_table"],
-                             ctx["dram_block_table"], *views)
-            attend = ops.sparse_tail_attention_mtp
-        else:
-            ops.scatter_copy(out["topk_src_ids"].view(B, TOPK), out["topk_dst_slots"].view(B, TOPK),
-                             out["miss_counts"], ctx["hbm_block_table"], ctx["dram_block_table"], *views)
-            attend = ops.sparse_tail_attention
+        attend = ops.sparse_tail_attention_mtp if self.mtp else ops.sparse_tail_attention
         attend(*common, ctx["hbm_block_table"], lay.hbm_k_rope, lay.hbm_kv_cache, scale, attention_out)
 
     def step(self, ctx: Mapping[str, torch.Tensor], layer_inputs: Callable[[int], Mapping[str, object]]) -> None:
@@ -239,8 +262,43 @@ class IndexShareDecodeStep:
         if missing:
             raise ValueError(f"decode context is missing: {missing}")
         self.begin_step()
+        if self.prefetch:
+            self._step_prefetch(ctx, layer_inputs)
+            return
         for i in range(self.groups.num_hidden_layers):
             self.run_layer(i, ctx, **layer_inputs(i))
+
+    def _step_prefetch(self, ctx, layer_inputs) -> None:
+        """Group prefetch: once an owner has selected, the copies of every
+        member of its group (they depend only on the owner's buffers) run on a
+        side stream, and each member's attention waits only for its own copy.
+        The copy stream starts after the previous step's work on the current
+        stream (the owner buffers and HBM slots it rewrites are free then) and
+        rejoins the current stream at the end, so the step is one unit for a
+        HIP graph capture."""
+        B = int(ctx["num_candidate_tokens"].shape[0])
+        dev = self.layers[0].hbm_kv_cache.device
+        main = torch.cuda.current_stream(dev)
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(device=dev)
+            self._events = [torch.cuda.Event() for _ in range(self.groups.num_hidden_layers + 1)]
+        cs, ev = self._copy_stream, self._events
+        cs.wait_stream(main)
+        for g in self.groups.groups():
+            kw = dict(layer_inputs(g.owner_layer_idx))
+            self._select(g.owner_layer_idx, ctx, B, kw.pop("query_index", None), kw.pop("index_weights", None))
+            ev[-1].record(main)
+            cs.wait_event(ev[-1])
+            with torch.cuda.stream(cs):
+                for m in g.member_layer_idxs:
+                    self._copy(m, ctx, B)
+                    ev[m].record(cs)
+            for m in g.member_layer_idxs:
+                if m != g.owner_layer_idx:
+                    kw = dict(layer_inputs(m))
+                main.wait_event(ev[m])
+                self._attend(m, ctx, B, kw["query_rope"], kw["query"], kw["scale"], kw["attention_out"], fused=False)
+        main.wait_stream(cs)
 
 
 __all__ = ["CONTEXT_FIELDS", "DsaLayerCaches", "IndexShareDecodeStep", "IndexShareGroup", "IndexShareGroupManager",

@@ -7,8 +7,9 @@ attend (reference glm_mla.py:1336-1406, :1542-1611).  Owner 0 starts from a
 pool with misses; owner 2 starts from owner 0's post-update pool with the
 same keys and query, so it selects the same tokens with no misses: a member
 wired to the wrong owner copies rows it must not and fails the bit-exact
-cache check.  Fused (``fused_copy_sfa(_mtp)``) and split
-(``scatter_copy`` + ``sparse_tail_attention(_mtp)``) paths, MTP0 and MTP3.
+cache check.  Fused (``fused_copy_sfa(_mtp)``), split (``scatter_copy`` +
+``sparse_tail_attention(_mtp)``) and group-prefetch (the split path with each
+group's copies on a side stream) modes, MTP0 and MTP3.
 """
 
 from __future__ import annotations
@@ -63,12 +64,13 @@ def _oracle_layer(case, caches, lim, mtp):
     return out, hkpe, hckv
 
 
-@pytest.mark.parametrize("mtp,fused", [(False, True), (False, False), (True, True), (True, False)])
-def test_index_share_step_matches_oracle(mtp, fused):
+@pytest.mark.parametrize("mtp", [False, True])
+@pytest.mark.parametrize("mode", ["fused", "split", "prefetch"])
+def test_index_share_step_matches_oracle(mtp, mode):
     from nanovllm_amd.index_share import CONTEXT_FIELDS, DsaLayerCaches, IndexShareDecodeStep, IndexShareGroupManager
     from nanovllm_amd.workloads import ChainCase, make_chain_case
 
-    print(f"INDEXSHARE mtp={mtp} fused={fused}", flush=True)
+    print(f"INDEXSHARE mtp={mtp} mode={mode}", flush=True)
     if mtp:
         case = make_chain_case(2, [9216, 12288], [8192, 9216], [4, 33], seed=41, mtp=True)
     else:
@@ -93,7 +95,7 @@ def test_index_share_step_matches_oracle(mtp, fused):
             own = dict(index_key_cache=d["index_key_cache"], cache_slots_pool=pool_b)
         layers.append(DsaLayerCaches(**dc, **own))
     groups = IndexShareGroupManager(4, TYPES)
-    runner = IndexShareDecodeStep(groups, layers, mtp=mtp, fused=fused)
+    runner = IndexShareDecodeStep(groups, layers, mtp=mtp, fused=mode == "fused", prefetch=mode == "prefetch")
     outs = [torch.full_like(d["attention_out"], 7.0) for _ in range(4)]
 
     def inputs(i):
@@ -116,4 +118,34 @@ def test_index_share_step_matches_oracle(mtp, fused):
         gold, hkpe, hckv = expect[i]
         assert np.array_equal(bits(layers[i].hbm_kv_cache), hckv), i
         assert np.array_equal(bits(layers[i].hbm_k_rope), hkpe), i
-        assert_attention_close(outs[i], gold, label=f"layer {i} mtp={mtp} fused={fused}")
+        assert_attention_close(outs[i], gold, label=f"layer {i} mtp={mtp} {mode}")
+
+    # The same step captured in one HIP graph (the prefetch mode forks a copy
+    # stream inside the capture): now every selection hits, and a replay must
+    # give exactly what the eager step gives on the same state.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        runner.step({f: d[f] for f in CONTEXT_FIELDS}, inputs)
+
+    def clear():
+        for o in outs:
+            o.fill_(7.0)
+        for owner in owner_lim:
+            for buf in runner.owner_outputs(owner, B).values():
+                buf.fill_(-5)
+
+    snap = []
+    for run in ("replay", "eager", "replay"):
+        clear()
+        if run == "replay":
+            graph.replay()
+        else:
+            runner.step({f: d[f] for f in CONTEXT_FIELDS}, inputs)
+        torch.cuda.synchronize()
+        snap.append([o.clone() for o in outs] + [b.clone() for owner in owner_lim
+                                                 for b in runner.owner_outputs(owner, B).values()])
+    assert int(runner.owner_outputs(0, B)["miss_counts"].sum()) == 0
+    for a, b in zip(snap[0], snap[1]):
+        assert torch.equal(a, b)
+    for a, b in zip(snap[2], snap[1]):
+        assert torch.equal(a, b)
