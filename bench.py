@@ -20,6 +20,9 @@ the miss copy and the CPU oracle on the same inputs are reported alongside.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 Prints one JSON line.
 
+``--row NAME`` measures one of the extra rows alone and prints its JSON
+object (the per-row kernel-trace profiles are taken this way).
+
 Two helper modes serve the hardware-counter runs whose summaries sit in
 profiles/: ``--kernels-only {lim,fused,split,sfa,copy} [--reps R]`` launches
 one kernel family alone on the same cfg1 inputs (``copy`` is the calibration
@@ -48,6 +51,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X published HBM3E bandwidth
 PCIE_PEAK_GBS = 64.0           # PCIe Gen5 x16 per direction (published)
 ROW_BYTES = (512 + 64) * 2     # one latent KV row (CKV + KPE)
 KEY_ROW_BYTES = 128 * 2        # one index-key row
+ROW_NAMES = ("cfg3_mtp3", "cfg2_bs64_mixed", "cfg4_indexshare", "lidu_init", "indexer_project", "prefill_persist")
 
 
 def log(msg: str) -> None:
@@ -65,6 +69,8 @@ def parse_args():
                    help="skip the per-row measurements (BASELINE configs[2]-[4], LIDU init, indexer "
                         "projection, prefill persist)")
     p.add_argument("--cpu-steps", type=int, default=8, help="layer-steps of the CPU oracle sample")
+    p.add_argument("--row", choices=ROW_NAMES, default=None,
+                   help="measure one row alone, print its JSON object and exit (for per-row profiles)")
     p.add_argument("--kernels-only", choices=("lim", "fused", "split", "sfa", "copy"), default=None,
                    help="launch one kernel family alone (for rocprofv3 --pmc) and exit")
     p.add_argument("--reps", type=int, default=4, help="launches in --kernels-only mode")
@@ -182,6 +188,15 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.row:
+        measure = {"cfg3_mtp3": lambda: measure_mtp3(torch, np, dev, args.seed),
+                   "cfg2_bs64_mixed": lambda: measure_cfg2(torch, np, dev, args.seed),
+                   "cfg4_indexshare": lambda: measure_cfg4(torch, np, dev, args.seed),
+                   "lidu_init": lambda: measure_lidu_init(torch, np, dev, args.seed),
+                   "indexer_project": lambda: measure_indexer(torch, dev, args.seed),
+                   "prefill_persist": lambda: measure_persist(torch, dev, args.seed)}[args.row]
+        print(json.dumps({"row": args.row, **measure()}), flush=True)
+        return 0
     if args.kernels_only == "copy":
         n = 64 << 20  # float32 elements: 256 MiB read and 256 MiB written per launch
         a = torch.ones(n, dtype=torch.float32, device=dev)
