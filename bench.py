@@ -82,7 +82,7 @@ def parse_args():
 # ---- hardware-counter helpers ------------------------------------------------
 PMC_KERNELS = ("lim_score_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
                "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel",
-               "sfa_combine_kernel", "scatter_copy_kernel")
+               "sfa_combine_kernel", "scatter_copy_kernel", "indexer_project_kernel")
 PMC_PROFILE = REPO / "profiles" / "lim_score_cfg1_pmc.txt"
 
 
