@@ -24,8 +24,9 @@
 //   bf16/f16 hi+lo pair so its rounding stays at fp32 level.  A second
 //   kernel merges the per-split (max, sum, numerator) partials.
 //   fused_copy_sfa (MTP0): a row's miss keys are the first miss_counts
-//   entries of its list.  The first kMissSplits splits of the row take the
-//   tiles holding them: each such tile is read once from host-mapped DRAM,
+//   entries of its list.  The first few splits of the row (kMissSplits, more
+//   at small batches) take the tiles holding them: each such tile is read
+//   once from host-mapped DRAM,
 //   stored to its HBM slots and consumed from LDS.  A split's host tiles are
 //   sequential (one PCIe round trip each).  The other splits take the
 //   HBM-only tiles, so the host-link-bound copy and the HBM-bound attention
@@ -54,7 +55,8 @@ constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per wi
 constexpr int kWindowKeys = kWindowTiles * kTileKeys;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxSlack = 8.f;  // base-2 headroom of the running max (P < 256)
-constexpr int kMissSplits = 2;  // fused: splits of a row that take its host-sourced tiles
+constexpr int kMissSplits = 2;  // fused: least splits of a row that take its host-sourced tiles
+constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgroups per launch
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -210,9 +212,15 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   int t_first = split, t_stride = splits, t_end = ntiles;
   const int mtiles = FUSED ? static_cast<int>(ceil_div(copy_count, kTileKeys)) : 0;
   if (FUSED && mtiles > 0 && splits >= 2) {  // (one split per row takes every tile)
-    // Two splits take the host-sourced tiles (measured best at cfg1; more
-    // of them leave too few splits for the row's HBM-resident tiles).
-    const int miss_splits = kMissSplits < splits - 1 ? kMissSplits : splits - 1;
+    // About kMissWorkgroups workgroups of the launch take host-sourced tiles:
+    // at least kMissSplits per row (measured best at 24 rows; more of them
+    // leave too few splits for the row's HBM-resident tiles), more per row at
+    // small batches (4 at 8 rows: 3% off the 78-layer step), never more than
+    // the row's miss tiles.
+    int miss_splits = static_cast<int>(ceil_div(kMissWorkgroups, a.batch * a.rows_per_request));
+    if (miss_splits > mtiles) miss_splits = mtiles;
+    if (miss_splits < kMissSplits) miss_splits = kMissSplits;
+    if (miss_splits > splits - 1) miss_splits = splits - 1;
     if (split < miss_splits) {
       t_first = split;
       t_stride = miss_splits;
