@@ -510,6 +510,31 @@ __device__ inline void load_score_keys(const float* s, int n, int t, uint32_t* k
   }
 }
 
+// Eight consecutive tokens [t0, t0 + 8): raw score bits and pool slots,
+// unconverted (tokens >= n: in = false, raw 0, slot -1).
+__device__ inline void load_raw8(const float* s, const int32_t* pool, int n, int t0, uint32_t* raw, int32_t* slot,
+                                 bool* in) {
+  if (t0 + kItems <= n) {
+    const uint4 a = *reinterpret_cast<const uint4*>(s + t0);
+    const uint4 b = *reinterpret_cast<const uint4*>(s + t0 + 4);
+    const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
+    const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
+    raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+    raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
+    slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
+    slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) in[e] = true;
+  } else {
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      in[e] = t0 + e < n;
+      raw[e] = in[e] ? __float_as_uint(s[t0 + e]) : 0u;
+      slot[e] = in[e] ? pool[t0 + e] : -1;
+    }
+  }
+}
+
 // Eight consecutive tokens [t0, t0 + 8): score keys and pool slots.
 __device__ inline void load_tokens8(const float* s, const int32_t* pool, int n, int t0, uint32_t* u, int32_t* slot,
                                     bool* in) {
@@ -847,7 +872,10 @@ __device__ inline SelectOut read_select(const LimWs& w, int64_t row) {
 
 // Classify eight consecutive candidates [t0, t0 + 8) of the ordered pass:
 // selection (with ascending-token tie ranks), misses appended in token order,
-// cached tokens recorded in the slot table.  Contains block scans.
+// cached tokens recorded in the slot table.  Contains block scans with
+// LDS-only barriers (so the caller's loads of the next tokens stay in
+// flight); the slot table and miss list are read only after the caller's
+// next full barrier.
 __device__ inline void mtp0_classify8(int t0, const uint32_t* u, const int32_t* slot, const bool* in, int c,
                                       const SelectOut& sel, bool need_rank, int& eq_run, int& miss_run,
                                       int32_t* misses, uint32_t* stab, uint32_t* skey, int* scratch) {
@@ -864,7 +892,7 @@ __device__ inline void mtp0_classify8(int t0, const uint32_t* u, const int32_t* 
   }
   if (need_rank) {
     int tot;
-    int rk = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
+    int rk = eq_run + block_exclusive_scan<true>(__popc(eqmask), scratch, &tot);
 #pragma unroll
     for (int e = 0; e < kItems; ++e)
       if ((eqmask >> e) & 1u) {
@@ -875,7 +903,7 @@ __device__ inline void mtp0_classify8(int t0, const uint32_t* u, const int32_t* 
   }
   const unsigned missmask = selmask & ~cachedmask;
   int tot;
-  int mp = miss_run + block_exclusive_scan(__popc(missmask), scratch, &tot);
+  int mp = miss_run + block_exclusive_scan<true>(__popc(missmask), scratch, &tot);
 #pragma unroll
   for (int e = 0; e < kItems; ++e) {
     if ((missmask >> e) & 1u) misses[mp++] = t0 + e;
@@ -1142,13 +1170,26 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   } else {
     const SelectOut sel = read_select(w, b);  // lim_threshold_kernel
     const bool need_rank = sel.cnt_eq != sel.need_eq;
+    // Software-pipelined: the next chunk's raw scores and slots are loaded
+    // before this chunk is classified, and converted to keys only when used.
+    uint32_t raw[kItems];
+    int32_t slot[kItems];
+    bool in[kItems];
+    load_raw8(s, pool, n, tid * kItems, raw, slot, in);
     for (int base = 0; base < n; base += kChunk) {
-      const int t0 = base + tid * kItems;
       uint32_t u[kItems];
-      int32_t slot[kItems];
-      bool in[kItems];
-      load_tokens8(s, pool, n, t0, u, slot, in);
-      mtp0_classify8(t0, u, slot, in, c, sel, need_rank, eq_run, miss_run, misses, stab, skey, scratch);
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) u[e] = in[e] ? score_key(__uint_as_float(raw[e])) : 0u;
+      int32_t cur_slot[kItems];
+      bool cur_in[kItems];
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) {
+        cur_slot[e] = slot[e];
+        cur_in[e] = in[e];
+      }
+      if (base + kChunk < n) load_raw8(s, pool, n, base + kChunk + tid * kItems, raw, slot, in);  // uniform
+      mtp0_classify8(base + tid * kItems, u, cur_slot, cur_in, c, sel, need_rank, eq_run, miss_run, misses, stab,
+                     skey, scratch);
     }
   }
   __syncthreads();

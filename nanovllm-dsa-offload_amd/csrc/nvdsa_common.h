@@ -95,9 +95,28 @@ __device__ inline uint32_t float_key(float f) {
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Workgroup barrier that orders LDS only: global loads still in flight stay
+// in flight across it (a __syncthreads() would wait for them first).
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <bool LDS_ONLY>
+__device__ inline void scan_barrier() {
+  if constexpr (LDS_ONLY)
+    lds_barrier();
+  else
+    __syncthreads();
+}
+
 // Block-wide exclusive prefix sum of one int per thread (blockDim <= 1024,
 // multiple of 64).  `scratch` must hold blockDim/64 + 1 ints.  Returns the
-// exclusive prefix; *total receives the block sum.  Contains __syncthreads.
+// exclusive prefix; *total receives the block sum.  Contains barriers: full
+// ones, or with LDS_ONLY barriers that order LDS only (for callers whose
+// global writes nobody reads before a later full barrier).
+template <bool LDS_ONLY = false>
 __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -110,7 +129,7 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
     if (lane >= d) x += y;
   }
   if (lane == 63) scratch[wid] = x;
-  __syncthreads();
+  scan_barrier<LDS_ONLY>();
   if (threadIdx.x == 0) {
     int run = 0;
     for (int w = 0; w < nw; ++w) {
@@ -120,10 +139,10 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
     }
     scratch[nw] = run;
   }
-  __syncthreads();
+  scan_barrier<LDS_ONLY>();
   int excl = scratch[wid] + x - v;
   *total = __builtin_amdgcn_readfirstlane(scratch[nw]);  // uniform: may steer barrier-containing code
-  __syncthreads();
+  scan_barrier<LDS_ONLY>();
   return excl;
 }
 
