@@ -176,7 +176,7 @@ def main() -> int:
         return summarize_pmc(args.summarize_pmc)
     if args.gpus != 1:
         log(f"bench.py measures one GPU only (got --gpus {args.gpus}): every box of this build has a single "
-            "MI355X; the multi-GPU sharding of this path is described in DESIGN.md, not benchmarked.")
+            "MI355X, so the sharding of this path over several GPUs is designed but not benchmarked.")
         return 2
 
     import numpy as np
