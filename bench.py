@@ -606,8 +606,7 @@ def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
             step(i)
             misses.append(int(t["miss_counts"].sum()))
     torch.cuda.synchronize()
-    km = _kernel_means(kt, ("lim_score_kernel", "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel_fused",
-                            "sfa_combine_kernel"))
+    km = _kernel_means(kt, ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel"))
     graph_us = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps)  # parity 0: an even number ran
     n_tokens = int(t["num_candidate_tokens"].sum())
     miss_rows = float(np.mean(misses))
@@ -693,8 +692,7 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
             step(i)
             misses.append(int(runner.owner_outputs(0, B)["miss_counts"].sum()))
     torch.cuda.synchronize()
-    names = ("lim_score_kernel", "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel_fused",
-             "sfa_combine_kernel")
+    names = ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel")
     km = _kernel_means(kt, names)
     per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names}
     graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran

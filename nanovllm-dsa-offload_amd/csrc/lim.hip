@@ -746,33 +746,15 @@ __device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t*
 }
 
 // ---------------------------------------------------------------------------
-// Top-2048 threshold of one (request, query) score row, written to the
-// workspace for a management kernel (MTP3, and MTP0 sources longer than the
-// manage kernel keeps in registers).  One workgroup per row; RES > 0 keeps
-// the row's keys in registers (RES chunks of 4096 tokens) for its radix
-// passes, RES == 0 streams them.
+// Top-2048 threshold of the score row s[0, n) (the row buffer holds cap >= n
+// entries).  RES > 0 keeps the row's keys in registers (RES chunks of 4096
+// tokens, n <= RES * kChunk) for the radix passes; RES == 0 streams them
+// from memory on every pass.  `hist` must be zero on entry and is zero again
+// on return.
 template <int RES>
-__global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a, LimWs w, int queries) {
-  __shared__ uint32_t hist[kBins];
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
-  __shared__ int bcast[4];
-  const int b = blockIdx.x / queries;
-  const int q = blockIdx.x - b * queries;
+__device__ __forceinline__ SelectOut row_threshold(const float* s, int n, int64_t cap, uint32_t* hist, int* scratch,
+                                                   int* bcast, uint32_t* red) {
   const int tid = threadIdx.x;
-  const int n = a.num_candidates[b];
-  const int c = a.num_cache[b];
-  const int r = a.pool_entries[b];
-  const bool valid = queries > 1 ? lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)
-                                 : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
-  if (!valid) return;
-  const int64_t cap = a.source_capacity;
-  const float* s = w.scores + (static_cast<int64_t>(b) * queries + q) * cap;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  SelectOut sel;
-  // Ties at the threshold go to the lowest tokens: a token with key ==
-  // thresh is selected iff token <= cutoff (INT_MAX when all ties are taken).
-  int cutoff = INT_MAX;
   if constexpr (RES > 0) {
     uint32_t u[RES][kItems];
 #pragma unroll
@@ -796,7 +778,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
         }
       }
     block_minmax(lo, hi, red);
-    sel = radix_select_visit(
+    return radix_select_visit(
         kTopK, lo, hi,
         [&](auto&& fn) {
 #pragma unroll
@@ -821,10 +803,37 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
         }
     }
     block_minmax(lo, hi, red);
-    sel = radix_select(
+    return radix_select(
         ngroups, kTopK, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); },
         hist, scratch, bcast);
   }
+}
+
+// Top-2048 threshold of one (request, query) score row, written to the
+// workspace for the MTP3 management kernels.  One workgroup per row; RES > 0
+// keeps the row's keys in registers (RES chunks of 4096 tokens).
+template <int RES>
+__global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a, LimWs w, int queries) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  const int b = blockIdx.x / queries;
+  const int q = blockIdx.x - b * queries;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  const bool valid = queries > 1 ? lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)
+                                 : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
+  if (!valid) return;
+  const int64_t cap = a.source_capacity;
+  const float* s = w.scores + (static_cast<int64_t>(b) * queries + q) * cap;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  const SelectOut sel = row_threshold<RES>(s, n, cap, hist, scratch, bcast, red);
+  // Ties at the threshold go to the lowest tokens: a token with key ==
+  // thresh is selected iff token <= cutoff (INT_MAX when all ties are taken).
+  int cutoff = INT_MAX;
   if (sel.need_eq != sel.cnt_eq) {  // ties at the threshold (rare): one ordered pass finds the last selected
     const int ngroups = static_cast<int>(ceil_div(n, 4));
     int before = 0;
@@ -856,15 +865,6 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
     uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
     for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   }
-}
-
-// The threshold of score row `row`, read as wave-uniform values (call with a
-// row index that is the same across the wave).
-__device__ inline SelectOut read_select(const LimWs& w, int64_t row) {
-  const uint32_t* p = w.select + row * 4;
-  return SelectOut{static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(p[0])),
-                   static_cast<int>(__builtin_amdgcn_readfirstlane(p[1])),
-                   static_cast<int>(__builtin_amdgcn_readfirstlane(p[2]))};
 }
 
 // ---------------------------------------------------------------------------
@@ -986,13 +986,17 @@ __device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int 
   if (tid == 0) a.miss_counts[b] = m;
 }
 
-// RES > 0: the request's scores live in registers, RES chunks of kChunk
-// tokens (thread t holds tokens ch*kChunk + 8t .. +8), read from memory once;
-// the radix passes then touch no memory.  RES == 0 streams the scores from
-// the workspace on every pass (any source length).
-template <int RES>
+// One workgroup per request; each request takes its path from its own
+// candidate count, whatever the table width:
+// * n <= RES * kChunk: the request's scores live in registers, RES chunks of
+//   kChunk tokens (thread t holds tokens ch*kChunk + 8t .. +8), read from
+//   memory once; the radix passes then touch no memory;
+// * longer rows: the top-2048 threshold first (keys in registers up to
+//   LONG_RES * kChunk tokens, streamed beyond), then an ordered pass that
+//   streams the scores and pool slots from memory.
+template <int RES, int LONG_RES>
 __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, LimWs w) {
-  static_assert(RES <= 8, "the packed classification scan holds eight chunks");
+  static_assert(RES > 0 && RES <= 8, "the packed classification scan holds eight chunks");
   __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint64_t scratch64[2 * (kManageThreads / 64)];
@@ -1023,7 +1027,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   int eq_run = 0, miss_run = 0;
-  if constexpr (RES > 0) {
+  if (n <= RES * kChunk) {
     // Scores and pool slots of all the request's tokens, loaded once.  A
     // slot is kept as 16 bits: 0 <= slot < C (C <= 16383) or 0xffff for
     // "not cached", which is all the ordered pass distinguishes.  Entries at
@@ -1168,7 +1172,11 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
     else
       write_items(stab, skey, kSlotStride + tid);
   } else {
-    const SelectOut sel = read_select(w, b);  // lim_threshold_kernel
+    SelectOut sel;
+    if (LONG_RES > 0 && n <= LONG_RES * kChunk)
+      sel = row_threshold<LONG_RES>(s, n, cap, hist, scratch, bcast, red);
+    else
+      sel = row_threshold<0>(s, n, cap, hist, scratch, bcast, red);
     const bool need_rank = sel.cnt_eq != sel.need_eq;
     // Software-pipelined: the next chunk's raw scores and slots are loaded
     // before this chunk is classified, and converted to keys only when used.
@@ -1629,11 +1637,11 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 mgrid(static_cast<uint32_t>(a.batch)), mblock(kManageThreads);
-  if (Q == 1 && a.source_capacity <= 8 * kChunk) {  // one kernel, candidates in registers
-    launch_kernel(kKernLimManage, lim_manage_kernel<8>, mgrid, mblock, stream, a, w);
+  if (Q == 1) {  // one kernel; each request picks its path from its own candidate count
+    launch_kernel(kKernLimManage, lim_manage_kernel<8, 16>, mgrid, mblock, stream, a, w);
     return hipGetLastError();
   }
-  // Thresholds first, one workgroup per (request, query) score row.
+  // MTP3: thresholds first, one workgroup per (request, query) score row.
   const dim3 tgrid(static_cast<uint32_t>(a.batch * Q));
   if (a.source_capacity <= 16 * kChunk) {
     launch_kernel(kKernLimThreshold, lim_threshold_kernel<16>, tgrid, mblock, stream, a, w, Q);
@@ -1642,16 +1650,12 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (Q > 1) {
-    const int parts = static_cast<int>(mtp_parts(a.source_capacity));
-    if (parts > kManageThreads) return hipErrorInvalidValue;  // pass B scans one part per thread
-    const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
-    launch_kernel(kKernLimMtpPassA, lim_mtp_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
-    launch_kernel(kKernLimMtpVictims, lim_mtp_victims_kernel, mgrid, mblock, stream, a, w, parts);
-    launch_kernel(kKernLimMtpPassB, lim_mtp_pass_b_kernel, pgrid, mblock, stream, a, w, parts);
-  } else {
-    launch_kernel(kKernLimManage, lim_manage_kernel<0>, mgrid, mblock, stream, a, w);
-  }
+  const int parts = static_cast<int>(mtp_parts(a.source_capacity));
+  if (parts > kManageThreads) return hipErrorInvalidValue;  // pass B scans one part per thread
+  const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
+  launch_kernel(kKernLimMtpPassA, lim_mtp_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
+  launch_kernel(kKernLimMtpVictims, lim_mtp_victims_kernel, mgrid, mblock, stream, a, w, parts);
+  launch_kernel(kKernLimMtpPassB, lim_mtp_pass_b_kernel, pgrid, mblock, stream, a, w, parts);
   return hipGetLastError();
 }
 

@@ -25,7 +25,6 @@ or pinned CPU tensors; the GPU reads them over the host link.
 from __future__ import annotations
 
 import ctypes
-import threading
 
 import torch
 
@@ -108,30 +107,17 @@ def _ref(d: _lib.NvdsaTensor):
     return ctypes.byref(d)
 
 
-class _Workspace:
-    """Per (device, stream) scratch buffer, grown on demand.
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Scratch memory for one operator call, from torch's caching allocator.
 
-    Calls on one stream are ordered, so they can share one buffer.  The
-    buffer comes from torch's caching allocator, which keeps it valid inside
-    captured graphs (a growth during capture lands in the graph's pool)."""
-
-    def __init__(self) -> None:
-        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
-        self._lock = threading.Lock()
-
-    def get(self, device: torch.device, nbytes: int) -> tuple[int, int]:
-        stream = torch.cuda.current_stream(device)
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
-        with self._lock:
-            buf = self._bufs.get(key)
-            if buf is None or buf.numel() < nbytes:
-                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-                self._bufs[key] = buf
-        return buf.data_ptr(), buf.numel()
-
-
-_LIM_WORKSPACE = _Workspace()   # fused_li_manage(_mtp)
-_ATTN_WORKSPACE = _Workspace()  # the attention entry points
+    The block is allocated on the current stream and released when the call
+    returns; the allocator reuses it only for work ordered after this call
+    on that stream, so the kernels may still be running when it is freed.
+    Under HIP-graph capture the block comes from the graph's private pool
+    and stays reserved for as long as the graph lives, so every captured
+    graph replays against its own workspace, whatever is captured or run
+    after it.  In steady state no call reaches hipMalloc."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
 def _stream_of(t: torch.Tensor) -> int:
@@ -147,8 +133,8 @@ def _fused_li_manage(query, index_weights, index_key_cache, index_block_table, n
     nbytes = _L.nvdsa_fused_li_manage_workspace_size(query.shape[0] if query.dim() else 0,
                                                      index_block_table.shape[-1] * 128 if index_block_table.dim() == 2 else 0,
                                                      query.shape[1] if query.dim() > 1 else 0)
-    ws, wsn = _LIM_WORKSPACE.get(query.device, nbytes)
-    _lib.check(_L.nvdsa_fused_li_manage(*map(_ref, descs), ws, wsn, _stream_of(query)))
+    ws = _workspace(query.device, nbytes)
+    _lib.check(_L.nvdsa_fused_li_manage(*map(_ref, descs), ws.data_ptr(), ws.numel(), _stream_of(query)))
 
 
 def _fused_li_manage_mtp(query, index_weights, index_key_cache, index_block_table, num_candidate_tokens,
@@ -161,8 +147,8 @@ def _fused_li_manage_mtp(query, index_weights, index_key_cache, index_block_tabl
     nbytes = _L.nvdsa_fused_li_manage_mtp_workspace_size(
         batch, index_block_table.shape[-1] * 128 if index_block_table.dim() == 2 else 0,
         query.shape[1] if query.dim() > 1 else 0)
-    ws, wsn = _LIM_WORKSPACE.get(query.device, nbytes)
-    _lib.check(_L.nvdsa_fused_li_manage_mtp(*map(_ref, descs), ws, wsn, _stream_of(query)))
+    ws = _workspace(query.device, nbytes)
+    _lib.check(_L.nvdsa_fused_li_manage_mtp(*map(_ref, descs), ws.data_ptr(), ws.numel(), _stream_of(query)))
 
 
 def _scatter_copy(src_ids, dst_slots, copy_counts, hbm_block_table, dram_block_table, hbm_k_rope, hbm_kv_cache,
@@ -172,11 +158,11 @@ def _scatter_copy(src_ids, dst_slots, copy_counts, hbm_block_table, dram_block_t
     _lib.check(_L.nvdsa_scatter_copy(*map(_ref, descs), _stream_of(hbm_kv_cache)))
 
 
-def _attention_workspace(query: torch.Tensor) -> tuple[int, int]:
+def _attention_workspace(query: torch.Tensor) -> torch.Tensor:
     rows = query.shape[0] if query.dim() == 3 else 0
     heads = query.shape[1] if query.dim() == 3 else 0
     nbytes = _L.nvdsa_sparse_tail_attention_workspace_size(rows, heads, 0)
-    return _ATTN_WORKSPACE.get(query.device, nbytes)
+    return _workspace(query.device, nbytes)
 
 
 def _sparse_tail_attention(query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv, num_cache_tokens,
@@ -185,9 +171,9 @@ def _sparse_tail_attention(query_rope, query, actual_seq_lengths_query, actual_s
     descs = [_D(t) for t in (query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv, num_cache_tokens,
                              topk_dst_slots, hbm_block_table, hbm_k_rope, hbm_kv_cache)]
     out = _D(attention_out)
-    ws, wsn = _attention_workspace(query)
-    _lib.check(_L.nvdsa_sparse_tail_attention(*map(_ref, descs), float(scale_value), _ref(out), ws, wsn,
-                                              _stream_of(query)))
+    ws = _attention_workspace(query)
+    _lib.check(_L.nvdsa_sparse_tail_attention(*map(_ref, descs), float(scale_value), _ref(out), ws.data_ptr(),
+                                              ws.numel(), _stream_of(query)))
 
 
 def _sparse_tail_attention_mtp(query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv,
@@ -196,9 +182,9 @@ def _sparse_tail_attention_mtp(query_rope, query, actual_seq_lengths_query, actu
     descs = [_D(t) for t in (query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv, num_cache_tokens,
                              topk_dst_slots, hbm_block_table, hbm_k_rope, hbm_kv_cache)]
     out = _D(attention_out)
-    ws, wsn = _attention_workspace(query)
-    _lib.check(_L.nvdsa_sparse_tail_attention_mtp(*map(_ref, descs), float(scale_value), _ref(out), ws, wsn,
-                                                  _stream_of(query)))
+    ws = _attention_workspace(query)
+    _lib.check(_L.nvdsa_sparse_tail_attention_mtp(*map(_ref, descs), float(scale_value), _ref(out), ws.data_ptr(),
+                                                  ws.numel(), _stream_of(query)))
 
 
 def _fused_copy_sfa(query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv, num_cache_tokens,
@@ -208,9 +194,9 @@ def _fused_copy_sfa(query_rope, query, actual_seq_lengths_query, actual_seq_leng
                              topk_dst_slots, topk_src_ids, miss_counts, hbm_block_table, dram_block_table,
                              hbm_k_rope, hbm_kv_cache, dram_k_rope, dram_kv_cache)]
     out = _D(attention_out)
-    ws, wsn = _attention_workspace(query)
-    _lib.check(_L.nvdsa_fused_copy_sfa(*map(_ref, descs), float(scale_value), _ref(out), ws, wsn,
-                                       _stream_of(query)))
+    ws = _attention_workspace(query)
+    _lib.check(_L.nvdsa_fused_copy_sfa(*map(_ref, descs), float(scale_value), _ref(out), ws.data_ptr(),
+                                       ws.numel(), _stream_of(query)))
 
 
 def _fused_copy_sfa_mtp(query_rope, query, actual_seq_lengths_query, actual_seq_lengths_kv, num_cache_tokens,
@@ -222,9 +208,9 @@ def _fused_copy_sfa_mtp(query_rope, query, actual_seq_lengths_query, actual_seq_
                              hbm_block_table, dram_block_table, hbm_k_rope, hbm_kv_cache, dram_k_rope,
                              dram_kv_cache)]
     out = _D(attention_out)
-    ws, wsn = _attention_workspace(query)
-    _lib.check(_L.nvdsa_fused_copy_sfa_mtp(*map(_ref, descs), float(scale_value), _ref(out), ws, wsn,
-                                           _stream_of(query)))
+    ws = _attention_workspace(query)
+    _lib.check(_L.nvdsa_fused_copy_sfa_mtp(*map(_ref, descs), float(scale_value), _ref(out), ws.data_ptr(),
+                                           ws.numel(), _stream_of(query)))
 
 
 def lidu_init_row(query, weights, index_cache, index_block_table, candidate_len, cache_tokens, cache_slots_row,
@@ -234,9 +220,10 @@ def lidu_init_row(query, weights, index_cache, index_block_table, candidate_len,
     rest = [_D(t) for t in (cache_slots_row, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table,
                             dram_block_table)]
     nbytes = _L.nvdsa_initialize_lidu_row_workspace_size(cache_slots_row.shape[0] if cache_slots_row.dim() else 0)
-    ws, wsn = _LIM_WORKSPACE.get(query.device, nbytes)
+    ws = _workspace(query.device, nbytes)
     _lib.check(_L.nvdsa_initialize_lidu_row(*map(_ref, descs), int(candidate_len), int(cache_tokens),
-                                            *map(_ref, rest), int(block_size), ws, wsn, _stream_of(query)))
+                                            *map(_ref, rest), int(block_size), ws.data_ptr(), ws.numel(),
+                                            _stream_of(query)))
 
 
 def lidu_init_row_shared(cache_slots_row, cache_tokens, hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table,
@@ -244,9 +231,9 @@ def lidu_init_row_shared(cache_slots_row, cache_tokens, hbm_kpe, hbm_ckv, dram_k
     """nvdsa_initialize_lidu_row_shared (synchronises the current stream once)."""
     descs = [_D(t) for t in (hbm_kpe, hbm_ckv, dram_kpe, dram_ckv, hbm_block_table, dram_block_table)]
     nbytes = _L.nvdsa_initialize_lidu_row_workspace_size(cache_slots_row.shape[0] if cache_slots_row.dim() else 0)
-    ws, wsn = _LIM_WORKSPACE.get(hbm_kpe.device, nbytes)
+    ws = _workspace(hbm_kpe.device, nbytes)
     _lib.check(_L.nvdsa_initialize_lidu_row_shared(_ref(_D(cache_slots_row)), int(cache_tokens), *map(_ref, descs),
-                                                   ws, wsn, _stream_of(hbm_kpe)))
+                                                   ws.data_ptr(), ws.numel(), _stream_of(hbm_kpe)))
 
 
 def _dsa_indexer_query_rope_inplace(q_inout, cos, sin, rope_dim) -> None:

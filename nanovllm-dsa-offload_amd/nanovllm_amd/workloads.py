@@ -43,6 +43,41 @@ def _bf16(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return x.to(dtype)
 
 
+_FILL_CHUNK = 1 << 22  # elements per independently seeded chunk of a parallel fill
+
+
+def randn_fill(shape, seed: int, dtype: torch.dtype, threads: int | None = None) -> torch.Tensor:
+    """N(0,1) values of ``shape`` rounded to ``dtype``, filled in parallel.
+
+    The tensor is cut into chunks of 2^22 elements, each drawn from its own
+    torch CPU generator seeded by (seed, chunk), so the result depends only
+    on the shape and the seed, not on the thread count.  Full-size
+    configurations hold gigabytes of latent KV; a single generator takes
+    about a minute for cfg2's, a pool of threads a few seconds."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    out = torch.empty(shape, dtype=dtype)
+    flat = out.view(-1)
+    n = flat.numel()
+    nchunks = (n + _FILL_CHUNK - 1) // _FILL_CHUNK
+
+    def job(i: int) -> None:
+        g = torch.Generator().manual_seed((int(seed) * 1000003 + i) & ((1 << 63) - 1))
+        lo = i * _FILL_CHUNK
+        hi = min(n, lo + _FILL_CHUNK)
+        flat[lo:hi].copy_(torch.randn(hi - lo, generator=g))
+
+    workers = max(1, min(16, threads or os.cpu_count() or 1, nchunks))
+    if workers == 1:
+        for i in range(nchunks):
+            job(i)
+    else:
+        with ThreadPoolExecutor(workers) as ex:
+            list(ex.map(job, range(nchunks)))
+    return out
+
+
 def _f64(t: torch.Tensor) -> np.ndarray:
     return t.to(torch.float64).numpy()
 
@@ -74,9 +109,16 @@ class ChainCase:
         return ChainCase(out, dict(self.meta))
 
 
-def _topk_order(scores: np.ndarray) -> np.ndarray:
+def _topk_order(scores: np.ndarray, head: int | None = None) -> np.ndarray:
+    """Token ids by descending score, ties to the lower id.  With ``head``,
+    only the first ``head`` entries of that order (exact: every token tied
+    with the head-th largest score takes part in the ordering)."""
     n = scores.shape[0]
-    return np.lexsort((np.arange(n), -scores))
+    if head is None or head >= n:
+        return np.lexsort((np.arange(n), -scores))
+    thr = np.partition(scores, n - head)[n - head]  # the head-th largest score
+    cand = np.nonzero(scores >= thr)[0]
+    return cand[np.lexsort((cand, -scores[cand]))][:head]
 
 
 def make_chain_case(
@@ -95,12 +137,24 @@ def make_chain_case(
     extra_pool_rows: int = 1,
     query_scale: float = 1.0,
     structured_scores: bool = False,
+    source_capacity: int | None = None,
+    table_pad: int = -1,
+    fast_fill: bool = False,
 ) -> ChainCase:
     """One layer step.  ``source_lens`` / ``cache_tokens`` / ``tails`` are
     per-request lists (or scalars); source lengths are whole 128-token
     blocks.  ``mtp`` builds four index/attention queries per request.
     ``structured_scores`` uses the reference's closed-form index (score ==
-    token id, ut_ops/test_fused_li_manage.py:146-173)."""
+    token id, ut_ops/test_fused_li_manage.py:146-173).
+
+    ``source_capacity`` widens the index block table and the slot pool to
+    that many tokens (a multiple of 128) instead of the longest source, as
+    the model runner does: it sizes the pool and pads every block table to
+    ceil(max_model_len / 128) columns (nanovllm/engine/model_runner.py:587-598,
+    :747-752; max_model_len = 65536 by default, nanovllm/config.py:68).
+    ``table_pad`` fills the block-table columns past a request's blocks (the
+    runner pads with 0).  ``fast_fill`` draws the large N(0,1) tensors with
+    :func:`randn_fill` (different values from the serial generator)."""
     B = int(batch)
     as_list = lambda v: [int(x) for x in (v if hasattr(v, "__len__") else [v] * B)]  # noqa: E731
     N = as_list(source_lens)
@@ -109,14 +163,26 @@ def make_chain_case(
     Q = MTP_Q if mtp else 1
     g = torch.Generator().manual_seed(seed)
     rng = np.random.default_rng(seed)
+    fill_seed = [seed * 16 + 1]
+
+    def randn(*shape) -> torch.Tensor:
+        """A large N(0,1) tensor in ``dtype`` (serial generator unless fast_fill)."""
+        if fast_fill:
+            fill_seed[0] += 1
+            return randn_fill(shape, fill_seed[0], dtype)
+        return torch.randn(*shape, generator=g).to(dtype)
 
     cols = max(1, math.ceil(max(N) / BLOCK))
+    if source_capacity is not None:
+        if source_capacity % BLOCK or source_capacity < cols * BLOCK:
+            raise ValueError(f"source_capacity {source_capacity} must be a multiple of {BLOCK} covering every source")
+        cols = source_capacity // BLOCK
     cap = cols * BLOCK
     # ---- index keys, paged -------------------------------------------------
     nblk = [math.ceil(n / BLOCK) for n in N]
     total_idx = max(1, sum(nblk))
     perm = torch.randperm(total_idx, generator=g).to(torch.int32)
-    index_table = torch.full((B, cols), -1, dtype=torch.int32)
+    index_table = torch.full((B, cols), table_pad, dtype=torch.int32)
     off = 0
     for b in range(B):
         index_table[b, : nblk[b]] = perm[off : off + nblk[b]]
@@ -142,7 +208,7 @@ def make_chain_case(
         weights[:, 0] = 1.0
         weights = weights.to(dtype)
     else:
-        key_cache = torch.randn(total_idx, BLOCK, 1, IDX, generator=g).to(dtype)
+        key_cache = randn(total_idx, BLOCK, 1, IDX)
         q_index = torch.randn(B * Q, index_heads, IDX, generator=g).to(dtype)
         weights = torch.rand(B * Q, index_heads, generator=g).to(dtype)
 
@@ -189,7 +255,7 @@ def make_chain_case(
             for _ in range(4 * n):
                 changed = False
                 for q in range(Q):
-                    order = _topk_order(s[q])
+                    order = _topk_order(s[q], TOPK + 1)
                     if n <= TOPK:
                         continue
                     a, z = order[TOPK - 1], order[TOPK]
@@ -207,7 +273,7 @@ def make_chain_case(
             cached_lists.append(np.zeros(0, np.int64))
             slot_lists.append(np.zeros(0, np.int64))
             continue
-        sel_rows = [np.sort(_topk_order(s[q])[:TOPK]) for q in range(Q)]
+        sel_rows = [np.sort(_topk_order(s[q], TOPK)) for q in range(Q)]
         if mtp:
             seen = set()
             union = []
@@ -257,26 +323,26 @@ def make_chain_case(
         slot_lists.append(slots)
 
     # ---- latent KV: DRAM (full prompt) and HBM (C slots + tail) ------------------
-    dram_table = torch.full((B, cols), -1, dtype=torch.int32)
+    dram_table = torch.full((B, cols), table_pad, dtype=torch.int32)
     dperm = torch.randperm(total_idx, generator=g).to(torch.int32)
     off = 0
     for b in range(B):
         dram_table[b, : nblk[b]] = dperm[off : off + nblk[b]]
         off += nblk[b]
-    dram_ckv = torch.randn(total_idx, BLOCK, CKV, generator=g).to(dtype)
-    dram_kpe = torch.randn(total_idx, BLOCK, KPE, generator=g).to(dtype)
+    dram_ckv = randn(total_idx, BLOCK, CKV)
+    dram_kpe = randn(total_idx, BLOCK, KPE)
     hlen = [C[b] + T[b] for b in range(B)]
     hblk = [max(1, math.ceil(h / BLOCK)) for h in hlen]
     hcols = max(hblk)
     total_h = sum(hblk)
     hperm = torch.randperm(total_h, generator=g).to(torch.int32)
-    hbm_table = torch.full((B, hcols), -1, dtype=torch.int32)
+    hbm_table = torch.full((B, hcols), table_pad, dtype=torch.int32)
     off = 0
     for b in range(B):
         hbm_table[b, : hblk[b]] = hperm[off : off + hblk[b]]
         off += hblk[b]
-    hbm_ckv = torch.randn(total_h, BLOCK, 1, CKV, generator=g).to(dtype)
-    hbm_kpe = torch.randn(total_h, BLOCK, 1, KPE, generator=g).to(dtype)
+    hbm_ckv = randn(total_h, BLOCK, 1, CKV)
+    hbm_kpe = randn(total_h, BLOCK, 1, KPE)
     hc = hbm_ckv.view(-1, CKV)
     hk = hbm_kpe.view(-1, KPE)
     dc = dram_ckv.view(-1, CKV)
@@ -340,27 +406,34 @@ def make_chain_case(
     return ChainCase(tensors, meta)
 
 
-def baseline_config(index: int, seed: int = 0, dtype: torch.dtype = torch.bfloat16, guard: bool = False) -> ChainCase:
+def baseline_config(index: int, seed: int = 0, dtype: torch.dtype = torch.bfloat16, guard: bool = False,
+                    source_capacity: int | None = None, table_pad: int = -1, fast_fill: bool = True) -> ChainCase:
     """The configurations of BASELINE.json ``configs`` (0..3) at full size.
 
     cfg0: bs=1, 20480-token prompt, tail 37, C=2048.
     cfg1: bs=24, 32768-token prompts, tails U[1,127], miss 5-15%, C=2048.
     cfg2: bs=64, prompts U[20K,64K] (whole blocks), C=2048 (fused path).
     cfg3: MTP3, bs=16 x 4 queries, 48K prompts, C=8192.
+
+    ``source_capacity`` / ``table_pad`` give the caller's table layout (see
+    :func:`make_chain_case`); by default the tables are as wide as the
+    longest source.
     """
     rng = np.random.default_rng(1000 + index)
+    kw = dict(seed=seed, dtype=dtype, guard=guard, source_capacity=source_capacity, table_pad=table_pad,
+              fast_fill=fast_fill)
     if index == 0:
-        return make_chain_case(1, 20480, 2048, 37, seed=seed, dtype=dtype, guard=guard, miss_frac=(0.1, 0.1))
+        return make_chain_case(1, 20480, 2048, 37, miss_frac=(0.1, 0.1), **kw)
     if index == 1:
         tails = rng.integers(1, 128, size=24)
-        return make_chain_case(24, 32768, 2048, tails, seed=seed, dtype=dtype, guard=guard)
+        return make_chain_case(24, 32768, 2048, tails, **kw)
     if index == 2:
         lens = (rng.integers(20480, 65536 + 1, size=64) // BLOCK) * BLOCK
         tails = rng.integers(1, 128, size=64)
-        return make_chain_case(64, lens, 2048, tails, seed=seed, dtype=dtype, guard=guard)
+        return make_chain_case(64, lens, 2048, tails, **kw)
     if index == 3:
         tails = rng.integers(4, 128, size=16)
-        return make_chain_case(16, 49152, 8192, tails, seed=seed, dtype=dtype, guard=guard, mtp=True)
+        return make_chain_case(16, 49152, 8192, tails, mtp=True, **kw)
     raise ValueError(f"no baseline config {index}")
 
 
