@@ -101,6 +101,37 @@ int nvdsa_fused_li_manage(const nvdsa_tensor* query,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/* Scratch bytes of nvdsa_fused_li_manage_noalloc on each GPU (32 MiB: batch
+ * 64 at a 65536-token source capacity fits). */
+#define NVDSA_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* nvdsa_fused_li_manage without a workspace argument and without allocating.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP-graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The scratch memory is a static array of
+ * NVDSA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until
+ * the process ends; its address is looked up once per device, on the first
+ * call (the tensors' device must be the current device).  The call itself
+ * reaches no hipMalloc/hipFree.  Arguments, checks, results and errors are
+ * those of nvdsa_fused_li_manage; a batch x source capacity whose scratch
+ * (nvdsa_fused_li_manage_workspace_size) exceeds the static size returns
+ * NVDSA_ERR_WORKSPACE before anything is launched.  Every call on one GPU
+ * uses the same scratch memory, and no state carries over between calls
+ * (the kernels initialise what they read), but calls that overlap on one GPU
+ * (different streams, or graphs replayed concurrently) race: order them. */
+int nvdsa_fused_li_manage_noalloc(const nvdsa_tensor* query,
+                                  const nvdsa_tensor* index_weights,
+                                  const nvdsa_tensor* index_key_cache,
+                                  const nvdsa_tensor* index_block_table,
+                                  const nvdsa_tensor* num_candidate_tokens,
+                                  const nvdsa_tensor* num_cache_tokens,
+                                  const nvdsa_tensor* req_pool_entries,
+                                  const nvdsa_tensor* cache_slots_pool,
+                                  const nvdsa_tensor* topk_src_ids,
+                                  const nvdsa_tensor* topk_dst_slots,
+                                  const nvdsa_tensor* miss_counts,
+                                  void* stream);
+
 /* Four-query (MTP3) variant: union of four top-2048 sets.
  * Replaces torch.ops.nanovllm_dsa.fused_li_manage_mtp
  * (reference: bindings/nanovllm_ops.cpp:652-658,

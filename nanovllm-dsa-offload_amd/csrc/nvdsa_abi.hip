@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -206,18 +207,55 @@ size_t nvdsa_fused_li_manage_mtp_workspace_size(int64_t batch, int64_t source_ca
   return nvdsa::lim_workspace_bytes(batch, source_capacity, nvdsa::kMtpQueries);
 }
 
-int nvdsa_fused_li_manage(const nvdsa_tensor* query, const nvdsa_tensor* index_weights,
-                          const nvdsa_tensor* index_key_cache, const nvdsa_tensor* index_block_table,
-                          const nvdsa_tensor* num_candidate_tokens, const nvdsa_tensor* num_cache_tokens,
-                          const nvdsa_tensor* req_pool_entries, const nvdsa_tensor* cache_slots_pool,
-                          const nvdsa_tensor* topk_src_ids, const nvdsa_tensor* topk_dst_slots,
-                          const nvdsa_tensor* miss_counts, void* workspace, size_t workspace_bytes,
-                          void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Scratch memory of nvdsa_fused_li_manage_noalloc: one copy of this array per
+// GPU the library runs on, held until the process ends.  Host code never
+// uses the array's name as an address; it uses the per-device pointer that
+// hipGetSymbolAddress returns (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[NVDSA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (the current device), looked up
+// once per device; nullptr with the error message set on failure.
+void* noalloc_scratch(int device, const char* op) {
+  if (device < 0 || device >= kMaxDevices) {
+    fail(NVDSA_ERR_DEVICE, (std::string(op) + ": device index out of range").c_str());
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      fail(NVDSA_ERR_RUNTIME,
+           (std::string(op) + ": hipGetSymbolAddress(scratch) failed: " + hipGetErrorString(e)).c_str());
+      return nullptr;
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  return g_scratch_ptr[device];
+}
+
+// fused_li_manage with the workspace given by the caller, or (noalloc) with
+// the library's static per-device scratch array.
+int fused_li_manage_impl(const char* op, const nvdsa_tensor* query, const nvdsa_tensor* index_weights,
+                         const nvdsa_tensor* index_key_cache, const nvdsa_tensor* index_block_table,
+                         const nvdsa_tensor* num_candidate_tokens, const nvdsa_tensor* num_cache_tokens,
+                         const nvdsa_tensor* req_pool_entries, const nvdsa_tensor* cache_slots_pool,
+                         const nvdsa_tensor* topk_src_ids, const nvdsa_tensor* topk_dst_slots,
+                         const nvdsa_tensor* miss_counts, void* workspace, size_t workspace_bytes, void* stream,
+                         bool noalloc) {
   const nvdsa_tensor* const all[] = {query, index_weights, index_key_cache, index_block_table,
                                      num_candidate_tokens, num_cache_tokens, req_pool_entries,
                                      cache_slots_pool, topk_src_ids, topk_dst_slots, miss_counts};
-  if (!all_nonnull(all)) return fail(NVDSA_ERR_ARG, "fused_li_manage: null tensor argument");
-  Check c("fused_li_manage");
+  if (!all_nonnull(all)) return fail(NVDSA_ERR_ARG, (std::string(op) + ": null tensor argument").c_str());
+  Check c(op);
   // ops/fused_li_manage/fused_li_manage_torch_adpt.h:18-92
   c.need(dims_are(query, 3), NVDSA_ERR_SHAPE, "query must be [B, N, 128]")
       .need(sz(query, 1) == 32 || sz(query, 1) == 64, NVDSA_ERR_SHAPE, "index head count must be 32 or 64")
@@ -263,9 +301,25 @@ int nvdsa_fused_li_manage(const nvdsa_tensor* query, const nvdsa_tensor* index_w
   const int64_t B = sz(query, 0);
   const int64_t cols = sz(index_block_table, 1);
   const size_t need = nvdsa::lim_workspace_bytes(B, cols * 128, 1);
+  if (noalloc && need > NVDSA_NOALLOC_SCRATCH_BYTES) {
+    const std::string msg = std::string(op) + ": batch " + std::to_string(B) + " x source capacity " +
+                            std::to_string(cols * 128) + " needs " + std::to_string(need) +
+                            " bytes of scratch, more than the static " +
+                            std::to_string(static_cast<size_t>(NVDSA_NOALLOC_SCRATCH_BYTES)) +
+                            " bytes; call nvdsa_fused_li_manage with a workspace";
+    return fail(NVDSA_ERR_WORKSPACE, msg.c_str());
+  }
   if (B == 0) return NVDSA_OK;
+  if (noalloc) {
+    int current = -1;
+    if (hipGetDevice(&current) != hipSuccess || current != query->device)
+      return fail(NVDSA_ERR_DEVICE, (std::string(op) + ": the tensors' device must be the current device").c_str());
+    workspace = noalloc_scratch(current, op);
+    if (workspace == nullptr) return NVDSA_ERR_RUNTIME;  // message set by noalloc_scratch
+    workspace_bytes = NVDSA_NOALLOC_SCRATCH_BYTES;
+  }
   if (workspace_bytes < need || workspace == nullptr)
-    return fail(NVDSA_ERR_WORKSPACE, "fused_li_manage: workspace too small");
+    return fail(NVDSA_ERR_WORKSPACE, (std::string(op) + ": workspace too small").c_str());
   nvdsa::LimArgs a{};
   a.query = query->data;
   a.weights = index_weights->data;
@@ -287,8 +341,34 @@ int nvdsa_fused_li_manage(const nvdsa_tensor* query, const nvdsa_tensor* index_w
   a.elem = elem_of(query);
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
-  return launch_status(nvdsa::launch_fused_li_manage(a, static_cast<hipStream_t>(stream)),
-                       "fused_li_manage");
+  return launch_status(nvdsa::launch_fused_li_manage(a, static_cast<hipStream_t>(stream)), op);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nvdsa_fused_li_manage(const nvdsa_tensor* query, const nvdsa_tensor* index_weights,
+                          const nvdsa_tensor* index_key_cache, const nvdsa_tensor* index_block_table,
+                          const nvdsa_tensor* num_candidate_tokens, const nvdsa_tensor* num_cache_tokens,
+                          const nvdsa_tensor* req_pool_entries, const nvdsa_tensor* cache_slots_pool,
+                          const nvdsa_tensor* topk_src_ids, const nvdsa_tensor* topk_dst_slots,
+                          const nvdsa_tensor* miss_counts, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  return fused_li_manage_impl("fused_li_manage", query, index_weights, index_key_cache, index_block_table,
+                              num_candidate_tokens, num_cache_tokens, req_pool_entries, cache_slots_pool,
+                              topk_src_ids, topk_dst_slots, miss_counts, workspace, workspace_bytes, stream, false);
+}
+
+int nvdsa_fused_li_manage_noalloc(const nvdsa_tensor* query, const nvdsa_tensor* index_weights,
+                                  const nvdsa_tensor* index_key_cache, const nvdsa_tensor* index_block_table,
+                                  const nvdsa_tensor* num_candidate_tokens, const nvdsa_tensor* num_cache_tokens,
+                                  const nvdsa_tensor* req_pool_entries, const nvdsa_tensor* cache_slots_pool,
+                                  const nvdsa_tensor* topk_src_ids, const nvdsa_tensor* topk_dst_slots,
+                                  const nvdsa_tensor* miss_counts, void* stream) {
+  return fused_li_manage_impl("fused_li_manage_noalloc", query, index_weights, index_key_cache, index_block_table,
+                              num_candidate_tokens, num_cache_tokens, req_pool_entries, cache_slots_pool,
+                              topk_src_ids, topk_dst_slots, miss_counts, nullptr, 0, stream, true);
 }
 
 int nvdsa_fused_li_manage_mtp(const nvdsa_tensor* query, const nvdsa_tensor* index_weights,

@@ -58,6 +58,7 @@ SIGNATURES = {
     "nvdsa_version": ([], ctypes.c_char_p),
     "nvdsa_fused_li_manage_workspace_size": ([_I64, _I64, _I64], _SZ),
     "nvdsa_fused_li_manage": ([_P] * 11 + [_VP, _SZ, _VP], ctypes.c_int),
+    "nvdsa_fused_li_manage_noalloc": ([_P] * 11 + [_VP], ctypes.c_int),
     "nvdsa_fused_li_manage_mtp_workspace_size": ([_I64, _I64, _I64], _SZ),
     "nvdsa_fused_li_manage_mtp": ([_P] * 13 + [_VP, _SZ, _VP], ctypes.c_int),
     "nvdsa_scatter_copy": ([_P] * 9 + [_VP], ctypes.c_int),
