@@ -5,17 +5,22 @@
 
 One step = one target layer of one stable decode step for the whole batch.
 Inputs are resident in HBM (DRAM KV in pinned host-mapped memory, as in
-serving) before the timed region.  The index query alternates between two
-calibrated queries whose top-2048 sets differ by each request's target miss
-fraction, so every step really misses and copies ~5-15% of its selection and
-no state is restored inside the timed region.  Steps are replayed from
-captured HIP graphs (the serving path; the reference times graph replays
-too), two consecutive layer-steps per graph replay (the serving graph spans
-every layer of a decode step, so its launch cost is shared by many
-layer-steps; one step per replay is reported as ``fuse_graph_1step``);
-eager timing, the split path (LIM -> scatter_copy -> SFA), per-kernel
-HIP-event timing, the roofline of the index-key scan, the host-link rate of
-the miss copy and the CPU oracle on the same inputs are reported alongside.
+serving) before the timed region, laid out as the model runner lays them
+out: block tables padded to ceil(max_model_len/128) = 512 columns and a
+65536-wide slot pool.  The index query alternates between two calibrated
+queries whose top-2048 sets differ by each request's target miss fraction,
+so every step really misses and copies ~5-15% of its selection and no state
+is restored inside the timed region.  Steps are replayed from captured HIP
+graphs (the serving path; the reference times graph replays too), two
+consecutive layer-steps per graph replay (the serving graph spans every
+layer of a decode step, so its launch cost is shared by many layer-steps;
+one step per replay is reported as ``fuse_graph_1step``).  Reported beside
+it: eager timing, the same step with tables only as wide as the prompts,
+the split path (LIM -> scatter_copy -> SFA) eager and graph-replayed,
+per-kernel HIP-event times, the roofline of the index-key scan, the
+host-link rate of the miss copy, the CPU baseline on the same inputs, and
+rows for the other BASELINE configs and for the shapes of the reference's
+published tables (README_ops.md:281-324, Ascend 910C figures as context).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 Prints one JSON line.
@@ -51,7 +56,8 @@ HBM_PEAK_GBS = 8000.0          # MI355X published HBM3E bandwidth
 PCIE_PEAK_GBS = 64.0           # PCIe Gen5 x16 per direction (published)
 ROW_BYTES = (512 + 64) * 2     # one latent KV row (CKV + KPE)
 KEY_ROW_BYTES = 128 * 2        # one index-key row
-ROW_NAMES = ("cfg3_mtp3", "cfg2_bs64_mixed", "cfg4_indexshare", "lidu_init", "indexer_project", "prefill_persist")
+ROW_NAMES = ("cfg0_bs1", "cfg3_mtp3", "cfg2_bs64_mixed", "cfg4_indexshare", "ref_lim_bs24_64k",
+             "ref_copysfa_bs24_4heads", "lidu_init", "indexer_project", "prefill_persist")
 
 
 def log(msg: str) -> None:
@@ -134,6 +140,256 @@ def pmc_traffic(kernel: str):
     return int(m.group(1)) if m else None
 
 
+class Chain:
+    """One layer-step's device tensors and its two alternating index queries.
+
+    The pool starts with the top-C of ``query_index``; step p uses
+    ``query_index_b`` for even p and ``query_index`` for odd p, so every step
+    misses its target fraction and the copies keep the HBM cache consistent.
+    ``parity`` is the parity of the next step."""
+
+    def __init__(self, t, scale: float) -> None:
+        from nanovllm_amd import dsa_offload_ops as ops
+
+        self.ops, self.t, self.scale = ops, t, scale
+        self.queries = [t["query_index_b"], t["query_index"]]
+        self.parity = 0
+        B = t["num_candidate_tokens"].shape[0]
+        self.src2d = t["topk_src_ids"].view(B, -1)
+        self.dst2d = t["topk_dst_slots"].view(B, -1)
+        self.kpe3 = t["hbm_k_rope"].view(-1, 128, 64)
+        self.ckv3 = t["hbm_kv_cache"].view(-1, 128, 512)
+
+    def lim(self, p: int) -> None:
+        t = self.t
+        self.ops.fused_li_manage(self.queries[p % 2], t["index_weights"], t["index_key_cache"],
+                                 t["index_block_table"], t["num_candidate_tokens"], t["num_cache_tokens"],
+                                 t["req_pool_entries"], t["cache_slots_pool"], t["topk_src_ids"],
+                                 t["topk_dst_slots"], t["miss_counts"])
+
+    def fused(self) -> None:
+        t = self.t
+        self.ops.fused_copy_sfa(t["query_rope"], t["query"], t["actual_seq_lengths_query"],
+                                t["actual_seq_lengths_kv"], t["num_cache_tokens"], t["topk_dst_slots"], self.src2d,
+                                t["miss_counts"], t["hbm_block_table"], t["dram_block_table"], t["hbm_k_rope"],
+                                t["hbm_kv_cache"], t["dram_k_rope"], t["dram_kv_cache"], self.scale,
+                                t["attention_out"])
+
+    def scatter(self) -> None:
+        t = self.t
+        self.ops.scatter_copy(self.src2d, self.dst2d, t["miss_counts"], t["hbm_block_table"], t["dram_block_table"],
+                              self.kpe3, self.ckv3, t["dram_k_rope"], t["dram_kv_cache"])
+
+    def sfa(self) -> None:
+        t = self.t
+        self.ops.sparse_tail_attention(t["query_rope"], t["query"], t["actual_seq_lengths_query"],
+                                       t["actual_seq_lengths_kv"], t["num_cache_tokens"], t["topk_dst_slots"],
+                                       t["hbm_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"], self.scale,
+                                       t["attention_out"])
+
+    def step(self, kind: str, p: int) -> None:
+        """kind: "fuse" (LIM -> fused_copy_sfa), "split" (LIM -> scatter_copy
+        -> sparse_tail_attention) or "lim" (fused_li_manage alone)."""
+        self.lim(p)
+        if kind == "fuse":
+            self.fused()
+        elif kind == "split":
+            self.scatter()
+            self.sfa()
+
+    def run(self, kind: str, n: int, miss_log=None) -> None:
+        for i in range(n):
+            self.step(kind, self.parity)
+            if miss_log is not None:
+                miss_log[i].copy_(self.t["miss_counts"])
+            self.parity ^= 1
+
+    def capture(self, torch, kind: str):
+        """(graph of step parity 0, graph of parity 1, graph of both in turn),
+        captured on a side stream after two eager steps there."""
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            self.run(kind, 2)
+            stream.synchronize()
+            singles = []
+            for p in (0, 1):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    self.step(kind, p)
+                singles.append(g)
+            pair = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(pair, stream=stream):
+                self.step(kind, 0)
+                self.step(kind, 1)
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        return singles, pair
+
+    def replay_singles(self, graphs, n: int) -> None:
+        for _ in range(n):
+            graphs[0][self.parity].replay()
+            self.parity ^= 1
+
+    def time_pairs(self, torch, graphs, steps: int):
+        """(ms per layer-step, wall ms per layer-step) of ``steps`` steps
+        replayed two per graph launch."""
+        singles, pair = graphs
+        if self.parity:
+            singles[1].replay()
+            self.parity = 0
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps // 2):
+            pair.replay()
+        if steps % 2:
+            singles[0].replay()
+            self.parity = 1
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, (time.perf_counter() - w0) * 1e3 / steps
+
+    def time_singles(self, torch, graphs, steps: int) -> float:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        self.replay_singles(graphs, steps)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    def time_eager(self, torch, kind: str, steps: int) -> float:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        self.run(kind, steps)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
+def _kernel_table(kt, names):
+    return {n: round(kt.mean_ms(n) * 1000, 2) for n in names}
+
+
+def measure_cfg0(torch, np, dev, seed: int, steps: int = 20):
+    """bs=1, one 20480-token prompt, tail 37, C=2048,
+    ~10% misses, on the model runner's table layout.  offload_split
+    (fused_li_manage -> scatter_copy -> sparse_tail_attention, the path the
+    config names) and offload_fuse, each replayed from HIP graphs (two
+    alternating steps per launch), with per-kernel times."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import caller_layout, make_drift_case
+
+    case = make_drift_case(1, 20480, 2048, [37], miss_frac=(0.1, 0.1), seed=seed, calib_device=dev)
+    d = case.to_device(dev)
+    ch = Chain(caller_layout(d.tensors), case.meta["scale"])
+    out = {"workload": "bs=1, prompt 20480, C=2048, tail 37, ~10% misses, model-runner table layout, "
+                       "HIP-graph replay"}
+    for kind in ("split", "fuse"):
+        graphs = ch.capture(torch, kind)
+        ms, _ = ch.time_pairs(torch, graphs, steps)
+        log_ = torch.zeros(steps, 1, dtype=torch.int32, device=dev)
+        with _lib.KernelTimer(capacity=16 * steps) as kt:
+            ch.run(kind, steps, miss_log=log_)
+        torch.cuda.synchronize()
+        names = ("lim_score_kernel", "lim_manage_kernel") + (
+            ("scatter_copy_kernel", "sfa_split_kernel", "sfa_combine_kernel") if kind == "split"
+            else ("sfa_split_kernel_fused", "sfa_combine_kernel"))
+        out[f"{kind}_step_us"] = round(ms * 1000, 2)
+        out[f"{kind}_kernels_us"] = _kernel_table(kt, names)
+        out["miss_rows_per_step"] = round(float(log_.sum()) / steps, 1)
+        del graphs
+    del ch, d, case
+    torch.cuda.empty_cache()
+    return out
+
+
+# Ascend 910C figures of the reference's own tables (README_ops.md:294, :321), for context only:
+# a different chip, 4 attention heads (TP=16) and 64K sources.
+REF_910C = {"lim_us": 408.069, "native_li_us": 349.100, "copysfa_ms": 0.122046, "serial_ms": 0.166218,
+            "scatter_ms": 0.056705, "sfa_ms": 0.116870}
+
+
+def measure_ref_lim(torch, np, dev, seed: int, steps: int = 20):
+    """fused_li_manage alone at the shape of the reference's published LIM
+    table (README_ops.md:281, :286-299): bs=24, 65536-token sources, C=8192,
+    32 index heads, ~100-200 misses per request (alternating calibrated
+    queries), HIP-graph replay.  The 910C figure is printed beside it as
+    context (another chip)."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import caller_layout, make_drift_case
+
+    case = make_drift_case(24, 65536, 8192, 64, miss_frac=(150 / 2048, 250 / 2048), seed=seed, calib_device=dev)
+    d = case.to_device(dev)
+    ch = Chain(caller_layout(d.tensors), case.meta["scale"])
+    # With C = 8192 the pool soon holds both alternating selections, so every
+    # replay starts from the same pool (restored outside the timed span), as
+    # the reference's perf script does (ut_ops/test_fused_li_manage_perf.py).
+    pool0 = ch.t["cache_slots_pool"].clone()
+
+    def restore():
+        ch.t["cache_slots_pool"].copy_(pool0)
+
+    us = _graph_step_us(torch, [lambda: ch.lim(0)], steps, prepare=restore)
+    with _lib.KernelTimer(capacity=16 * steps) as kt:
+        for _ in range(steps):
+            restore()
+            ch.lim(0)
+    torch.cuda.synchronize()
+    n_tokens = 24 * 65536
+    km = _kernel_table(kt, ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel"))
+    out = {"workload": "fused_li_manage alone: bs=24, sources 65536, C=8192, 32 index heads, "
+                       "model-runner table layout, pool restored before each HIP-graph replay",
+           "step_us": round(us, 2), "kernels_us": km,
+           "miss_rows_per_request": round(float(ch.t["miss_counts"].float().mean()), 1),
+           "lim_score_hbm_GBs": round((n_tokens * (KEY_ROW_BYTES + 4)) / (km["lim_score_kernel"] * 1e-6) / 1e9, 1),
+           "ascend_910c_context_us": {"fused_li_manage": REF_910C["lim_us"], "native_li": REF_910C["native_li_us"]}}
+    del ch, d, case
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_ref_copysfa(torch, np, dev, seed: int, steps: int = 20):
+    """fused_copy_sfa at the shape of the reference's published COPYSFA
+    table (README_ops.md:307-324): bs=24, 4 attention heads (one TP=16
+    rank), 65536-token sources, C=8192, tail 64, ~100-200 misses per
+    request.  One LIM call makes the selection; then the fused op, the
+    serial pair (scatter_copy then sparse_tail_attention) and each alone are
+    replayed from HIP graphs on that selection (every replay copies the same
+    miss rows), as the reference's perf script times them.  910C figures
+    beside it as context."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import caller_layout, make_drift_case
+
+    case = make_drift_case(24, 65536, 8192, 64, attn_heads=4, miss_frac=(150 / 2048, 250 / 2048), seed=seed,
+                           calib_device=dev)
+    d = case.to_device(dev)
+    ch = Chain(caller_layout(d.tensors), case.meta["scale"])
+    ch.run("lim", 1)
+    torch.cuda.synchronize()
+    miss = float(ch.t["miss_counts"].float().mean())
+    fns = {"copysfa": ch.fused, "serial": lambda: (ch.scatter(), ch.sfa()), "scatter": ch.scatter, "sfa": ch.sfa}
+    out = {"workload": "bs=24, 4 attention heads, sources 65536, C=8192, tail 64, model-runner table layout, "
+                       "HIP-graph replay",
+           "miss_rows_per_request": round(miss, 1)}
+    for name, fn in fns.items():
+        out[f"{name}_us"] = round(_graph_step_us(torch, [fn], steps), 2)
+    with _lib.KernelTimer(capacity=16 * steps) as kt:
+        for _ in range(steps):
+            ch.fused()
+    torch.cuda.synchronize()
+    out["kernels_us"] = _kernel_table(kt, ("sfa_split_kernel_fused", "sfa_combine_kernel"))
+    copy_bytes = float(ch.t["miss_counts"].sum()) * ROW_BYTES
+    out["fused_h2d_GBs"] = round(copy_bytes / (out["kernels_us"]["sfa_split_kernel_fused"] * 1e-6) / 1e9, 2)
+    out["ascend_910c_context_ms"] = {k: v for k, v in REF_910C.items() if k.endswith("_ms")}
+    del ch, d, case
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_h2d_peak(torch, dev) -> float:
     """Pinned host -> device hipMemcpyAsync rate of a 256 MiB transfer, GB/s."""
     n = 256 << 20
@@ -184,18 +440,12 @@ def main() -> int:
 
     from nanovllm_amd import _lib
     from nanovllm_amd import dsa_offload_ops as ops
-    from nanovllm_amd.workloads import make_drift_case
+    from nanovllm_amd.workloads import caller_layout, make_drift_case
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.row:
-        measure = {"cfg3_mtp3": lambda: measure_mtp3(torch, np, dev, args.seed),
-                   "cfg2_bs64_mixed": lambda: measure_cfg2(torch, np, dev, args.seed),
-                   "cfg4_indexshare": lambda: measure_cfg4(torch, np, dev, args.seed),
-                   "lidu_init": lambda: measure_lidu_init(torch, np, dev, args.seed),
-                   "indexer_project": lambda: measure_indexer(torch, dev, args.seed),
-                   "prefill_persist": lambda: measure_persist(torch, dev, args.seed)}[args.row]
-        print(json.dumps({"row": args.row, **measure()}), flush=True)
+        print(json.dumps({"row": args.row, **ROW_FUNCS[args.row](torch, np, dev, args.seed)}), flush=True)
         return 0
     if args.kernels_only == "copy":
         n = 64 << 20  # float32 elements: 256 MiB read and 256 MiB written per launch
@@ -215,158 +465,71 @@ def main() -> int:
         f"{[round(x, 3) for x in case.meta['drift_miss_frac']]}")
     cpu_case = case
     d = case.to_device(dev)
-    t = d.tensors
-    queries = [t["query_index_b"], t["query_index"]]  # pool holds top-C of query_index
     scale = case.meta["scale"]
-    src2d = t["topk_src_ids"].view(B, -1)
-    dst2d = t["topk_dst_slots"].view(B, -1)
-    kpe3 = t["hbm_k_rope"].view(-1, 128, 64)
-    ckv3 = t["hbm_kv_cache"].view(-1, 128, 512)
-
-    def lim(i):
-        ops.fused_li_manage(queries[i % 2], t["index_weights"], t["index_key_cache"], t["index_block_table"],
-                            t["num_candidate_tokens"], t["num_cache_tokens"], t["req_pool_entries"],
-                            t["cache_slots_pool"], t["topk_src_ids"], t["topk_dst_slots"], t["miss_counts"])
-
-    def fused():
-        ops.fused_copy_sfa(t["query_rope"], t["query"], t["actual_seq_lengths_query"], t["actual_seq_lengths_kv"],
-                           t["num_cache_tokens"], t["topk_dst_slots"], src2d, t["miss_counts"], t["hbm_block_table"],
-                           t["dram_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"], t["dram_k_rope"],
-                           t["dram_kv_cache"], scale, t["attention_out"])
-
-    def scatter():
-        ops.scatter_copy(src2d, dst2d, t["miss_counts"], t["hbm_block_table"], t["dram_block_table"], kpe3, ckv3,
-                         t["dram_k_rope"], t["dram_kv_cache"])
-
-    def sfa():
-        ops.sparse_tail_attention(t["query_rope"], t["query"], t["actual_seq_lengths_query"],
-                                  t["actual_seq_lengths_kv"], t["num_cache_tokens"], t["topk_dst_slots"],
-                                  t["hbm_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"], scale, t["attention_out"])
-
-    def fuse_step(i):
-        lim(i)
-        fused()
-
-    def split_step(i):
-        lim(i)
-        scatter()
-        sfa()
-
+    # The headline runs on the model runner's table layout: every block table
+    # padded with 0 to 512 columns and a 65536-wide slot pool (S_cap 65536).
+    t = caller_layout(d.tensors)
+    head = Chain(t, scale)
     if args.kernels_only:
-        lim(0)
-        fused()
+        head.run("fuse", 2)
         torch.cuda.synchronize()
         for i in range(args.reps):
             if args.kernels_only == "lim":
-                lim(i + 1)
+                head.run("lim", 1)
             elif args.kernels_only == "fused":
-                fuse_step(i + 1)
+                head.run("fuse", 1)
             elif args.kernels_only == "split":
-                split_step(i + 1)
+                head.run("split", 1)
             else:
-                sfa()
+                head.sfa()
         torch.cuda.synchronize()
         log(f"bench: kernels-only {args.kernels_only} done, {args.reps} launches, "
             f"last misses {int(t['miss_counts'].sum())}")
         return 0
 
     miss_log = torch.zeros(args.steps, B, dtype=torch.int32, device=dev)
-
-    # ---- warmup (eager; also allocates the op workspaces) -------------------
-    for i in range(max(args.warmup, 2)):
-        fuse_step(i)
+    head.run("fuse", max(args.warmup, 2))  # eager warmup
+    torch.cuda.synchronize()
+    fuse_graphs = head.capture(torch, "fuse")
+    head.replay_singles(fuse_graphs, args.warmup)
     torch.cuda.synchronize()
 
-    # ---- capture the two alternating steps as HIP graphs --------------------
-    # graphs[0] / graphs[1]: one layer-step each (query parity 0 / 1);
-    # pair: both steps in one graph.  The serving graph covers every layer
-    # of a decode step, so its launch cost is spread over many layer-steps;
-    # the timed region replays the two-step graph (K even), and the
-    # one-step-per-graph rate is reported beside it.
-    stream = torch.cuda.Stream()
-    graphs = []
-    with torch.cuda.stream(stream):
-        for i in range(2):  # warm the side stream (workspace per stream)
-            fuse_step(i)
-        stream.synchronize()
-        for i in range(2):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                fuse_step(i)
-            graphs.append(g)
-        pair = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(pair, stream=stream):
-            fuse_step(0)
-            fuse_step(1)
-    torch.cuda.synchronize()
-    # the captures ran nothing; the pool now holds top-C of query_index again
-    # only if an even number of eager steps ran: replay from step parity 0.
-    start_parity = (max(args.warmup, 2) + 2) % 2
-    for i in range(args.warmup):
-        graphs[(start_parity + i) % 2].replay()
-    torch.cuda.synchronize()
-    parity = (start_parity + args.warmup) % 2
-    if parity:  # the pair graph starts at parity 0
-        graphs[1].replay()
-        torch.cuda.synchronize()
-
-    # ---- timed region: K graph-replayed layer steps ------------------------
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    ev0.record()
-    for i in range(args.steps // 2):
-        pair.replay()
-    if args.steps % 2:
-        graphs[0].replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall1 = time.perf_counter()
-    graph_ms = ev0.elapsed_time(ev1) / args.steps
-    # one layer-step per graph replay, for reference
-    p1 = args.steps % 2
-    ev0.record()
-    for i in range(args.steps):
-        graphs[(p1 + i) % 2].replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    graph1_ms = ev0.elapsed_time(ev1) / args.steps
-    parity_after = (p1 + args.steps) % 2
-
-    # ---- eager fused steps -------------------------------------------------
-    parity = parity_after
-    ev0.record()
-    for i in range(args.steps):
-        fuse_step(parity + i)
-    ev1.record()
-    torch.cuda.synchronize()
-    eager_ms = ev0.elapsed_time(ev1) / args.steps
-    parity = (parity + args.steps) % 2
+    # ---- timed region: K graph-replayed layer steps (two per replay) --------
+    graph_ms, wall_ms = head.time_pairs(torch, fuse_graphs, args.steps)
+    graph1_ms = head.time_singles(torch, fuse_graphs, args.steps)
+    eager_ms = head.time_eager(torch, "fuse", args.steps)
 
     # ---- per-kernel HIP-event timing (eager, instrumented) ------------------
     with _lib.KernelTimer(capacity=16 * args.steps) as kt_fuse:
-        for i in range(args.steps):
-            fuse_step(parity + i)
-            miss_log[i].copy_(t["miss_counts"])
+        head.run("fuse", args.steps, miss_log=miss_log)
     torch.cuda.synchronize()
     misses = miss_log.cpu().numpy()
     miss_rows = float(misses.sum()) / args.steps
     miss_frac = miss_rows / (B * 2048)
-    parity = (parity + args.steps) % 2
     with _lib.KernelTimer(capacity=16 * args.steps) as kt_split:
-        for i in range(args.steps):
-            split_step(parity + i)
+        head.run("split", args.steps)
     torch.cuda.synchronize()
-    parity = (parity + args.steps) % 2
-    ev0.record()
-    for i in range(args.steps):
-        split_step(parity + i)
-    ev1.record()
-    torch.cuda.synchronize()
-    split_ms = ev0.elapsed_time(ev1) / args.steps
+    split_ms = head.time_eager(torch, "split", args.steps)
+    split_graphs = head.capture(torch, "split")
+    split_graph_ms, _ = head.time_pairs(torch, split_graphs, args.steps)
+    del fuse_graphs, split_graphs
 
-    k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused",
-                                                  "sfa_combine_kernel")}
+    # ---- the same step with tables only as wide as the prompts (S_cap 32768):
+    # its own pool and HBM caches, so both layouts start from the same state.
+    tn = dict(d.tensors)
+    tn["hbm_kv_cache"] = tn["hbm_kv_cache"].clone()
+    tn["hbm_k_rope"] = tn["hbm_k_rope"].clone()
+    narrow = Chain(tn, scale)
+    narrow.run("fuse", 2)
+    narrow_graphs = narrow.capture(torch, "fuse")
+    narrow_ms, _ = narrow.time_pairs(torch, narrow_graphs, args.steps)
+    with _lib.KernelTimer(capacity=16 * args.steps) as kt_narrow:
+        narrow.run("fuse", args.steps)
+    torch.cuda.synchronize()
+    del narrow_graphs, narrow, tn
+
+    k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel",
+                                                  "sfa_split_kernel_fused", "sfa_combine_kernel")}
     ks = {name: kt_split.mean_ms(name) for name in ("scatter_copy_kernel", "sfa_split_kernel")}
 
     # ---- roofline of the index-key scan (lim_score_kernel) ------------------
@@ -390,7 +553,7 @@ def main() -> int:
 
     rows = None
     if not args.no_rows:
-        del d, t, queries, graphs, case
+        del d, t, head, case
         torch.cuda.empty_cache()
         rows = {"cfg1": {"lim_score_us": round(k["lim_score_kernel"] * 1000, 2),
                          "lim_manage_us": round(k["lim_manage_kernel"] * 1000, 2),
@@ -401,14 +564,11 @@ def main() -> int:
                          "fused_split_us": round(k["sfa_split_kernel_fused"] * 1000, 2),
                          "fused_h2d_GBs": round(fused_h2d, 2),
                          "combine_us": round(k["sfa_combine_kernel"] * 1000, 2)}}
-        rows["cfg3_mtp3"] = measure_mtp3(torch, np, dev, args.seed)
-        rows["cfg2_bs64_mixed"] = measure_cfg2(torch, np, dev, args.seed)
-        rows["cfg4_indexshare"] = measure_cfg4(torch, np, dev, args.seed)
-        rows["lidu_init"] = measure_lidu_init(torch, np, dev, args.seed)
-        rows["indexer_project"] = measure_indexer(torch, dev, args.seed)
-        rows["prefill_persist"] = measure_persist(torch, dev, args.seed)
+        for name in ROW_NAMES:
+            rows[name] = ROW_FUNCS[name](torch, np, dev, args.seed)
 
     value_us = graph_ms * 1000.0
+    t_cap = 65536
     line = {
         "metric": METRIC,
         "value": round(value_us, 2),
@@ -425,8 +585,10 @@ def main() -> int:
         "config": {
             "workload": "BASELINE configs[1]: offload_fuse layer-step (fused_li_manage -> fused_copy_sfa), "
                         "bs=24, prompts 32768, C=2048, tails U[1,127], 32 index heads x 128, 64 attn heads "
-                        "512+64, miss 5-15%/request, HIP-graph replay",
+                        "512+64, miss 5-15%/request, model-runner table layout (512-column block tables, "
+                        "65536-wide slot pool), HIP-graph replay",
             "batch": B, "prompt_tokens": N, "cache_tokens": C, "index_heads": 32, "attn_heads": 64,
+            "source_capacity": int(t_cap),
             "mean_tail": float(np.mean(tails)), "mean_miss_rows_per_step": round(miss_rows, 1),
             "miss_fraction": round(miss_frac, 4),
         },
@@ -444,13 +606,17 @@ def main() -> int:
         "breakdown_us": {
             "fuse_graph_step": round(value_us, 2), "fuse_graph_1step": round(graph1_ms * 1000, 2),
             "fuse_eager_step": round(eager_ms * 1000, 2),
+            "fuse_graph_step_narrow_tables": round(narrow_ms * 1000, 2),
+            "lim_manage_narrow_tables": round(kt_narrow.mean_ms("lim_manage_kernel") * 1000, 2),
+            "split_graph_step": round(split_graph_ms * 1000, 2),
             "split_eager_step": round(split_ms * 1000, 2),
             "lim_score": round(k["lim_score_kernel"] * 1000, 2), "lim_manage": round(k["lim_manage_kernel"] * 1000, 2),
+            "lim_manage_long_empty": round(k["lim_manage_long_kernel"] * 1000, 2),
             "fused_copy_sfa_split": round(k["sfa_split_kernel_fused"] * 1000, 2),
             "sfa_combine": round(k["sfa_combine_kernel"] * 1000, 2),
             "scatter_copy": round(ks["scatter_copy_kernel"] * 1000, 2), "sfa_split": round(ks["sfa_split_kernel"] * 1000, 2),
             "sfa_hbm_GBs": round(sfa_ach, 1), "measured_hbm_copy_GBs": round(hbm_copy, 1),
-            "wall_us_per_step": round((wall1 - wall0) / args.steps * 1e6, 2),
+            "wall_us_per_step": round(wall_ms * 1000, 2),
         },
         "cpu_baseline": cpu,
         "rows": rows,
@@ -606,7 +772,8 @@ def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
             step(i)
             misses.append(int(t["miss_counts"].sum()))
     torch.cuda.synchronize()
-    km = _kernel_means(kt, ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel"))
+    km = _kernel_means(kt, ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel", "sfa_split_kernel_fused",
+                            "sfa_combine_kernel"))
     graph_us = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps)  # parity 0: an even number ran
     n_tokens = int(t["num_candidate_tokens"].sum())
     miss_rows = float(np.mean(misses))
@@ -692,7 +859,8 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
             step(i)
             misses.append(int(runner.owner_outputs(0, B)["miss_counts"].sum()))
     torch.cuda.synchronize()
-    names = ("lim_score_kernel", "lim_manage_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel")
+    names = ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel", "sfa_split_kernel_fused",
+             "sfa_combine_kernel")
     km = _kernel_means(kt, names)
     per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names}
     graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran
@@ -930,6 +1098,19 @@ def cpu_baseline(case, queries_cpu, steps: int):
         "sample": f"median of {steps} full cfg1 layer-steps (24 requests, LIM + fused copy/attention) of the "
                   f"numpy oracle after 1 warmup, same inputs; BLAS threads={threads}, os.cpu_count={os.cpu_count()}",
     }
+
+
+ROW_FUNCS = {
+    "cfg0_bs1": measure_cfg0,
+    "cfg3_mtp3": measure_mtp3,
+    "cfg2_bs64_mixed": measure_cfg2,
+    "cfg4_indexshare": measure_cfg4,
+    "ref_lim_bs24_64k": measure_ref_lim,
+    "ref_copysfa_bs24_4heads": measure_ref_copysfa,
+    "lidu_init": measure_lidu_init,
+    "indexer_project": lambda torch, np, dev, seed: measure_indexer(torch, dev, seed),
+    "prefill_persist": lambda torch, np, dev, seed: measure_persist(torch, dev, seed),
+}
 
 
 if __name__ == "__main__":

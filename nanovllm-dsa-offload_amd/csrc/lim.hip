@@ -986,15 +986,18 @@ __device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int 
   if (tid == 0) a.miss_counts[b] = m;
 }
 
-// One workgroup per request; each request takes its path from its own
-// candidate count, whatever the table width:
-// * n <= RES * kChunk: the request's scores live in registers, RES chunks of
-//   kChunk tokens (thread t holds tokens ch*kChunk + 8t .. +8), read from
-//   memory once; the radix passes then touch no memory;
-// * longer rows: the top-2048 threshold first (keys in registers up to
-//   LONG_RES * kChunk tokens, streamed beyond), then an ordered pass that
-//   streams the scores and pool slots from memory.
-template <int RES, int LONG_RES>
+// MTP0 management, one workgroup per request.  Each request takes its path
+// from its own candidate count n, whatever the table width:
+// * lim_manage_kernel<RES> takes the rows with n <= RES * kChunk: their
+//   scores live in registers, RES chunks of kChunk tokens (thread t holds
+//   tokens ch*kChunk + 8t .. +8), read from memory once; the radix passes
+//   then touch no memory.  It also answers every invalid row (miss_counts 0).
+// * lim_manage_long_kernel takes the longer rows (launched only when the
+//   table is wider than RES * kChunk tokens): the top-2048 threshold first,
+//   then an ordered pass that streams the scores and pool slots.
+// The two live in separate kernels: in one, the register path's arrays end
+// up in scratch memory (2.5x slower).
+template <int RES>
 __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, LimWs w) {
   static_assert(RES > 0 && RES <= 8, "the packed classification scan holds eight chunks");
   __shared__ uint32_t hist[kBins];
@@ -1015,6 +1018,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
     if (tid == 0) a.miss_counts[b] = 0;
     return;
   }
+  if (n > RES * kChunk) return;  // lim_manage_long_kernel's row
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + static_cast<int64_t>(b) * cap;
   int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
@@ -1027,7 +1031,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
   for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   int eq_run = 0, miss_run = 0;
-  if (n <= RES * kChunk) {
+  {
     // Scores and pool slots of all the request's tokens, loaded once.  A
     // slot is kept as 16 bits: 0 <= slot < C (C <= 16383) or 0xffff for
     // "not cached", which is all the ordered pass distinguishes.  Entries at
@@ -1171,12 +1175,43 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, L
       write_items(lds_stab, lds_skey, kLdsSlots + tid);
     else
       write_items(stab, skey, kSlotStride + tid);
-  } else {
-    SelectOut sel;
-    if (LONG_RES > 0 && n <= LONG_RES * kChunk)
-      sel = row_threshold<LONG_RES>(s, n, cap, hist, scratch, bcast, red);
-    else
-      sel = row_threshold<0>(s, n, cap, hist, scratch, bcast, red);
+  }
+  __syncthreads();
+  mtp0_finish(a, b, c, miss_run, pool, stab, skey, misses, vslot, hist, scratch, bcast, red);
+}
+
+// The rows longer than SHORT * kChunk candidates (see lim_manage_kernel):
+// threshold with the keys in registers (TRES chunks, TRES * kChunk >= every
+// such row) or streamed (TRES == 0), then the streamed ordered pass.
+template <int SHORT, int TRES>
+__global__ __launch_bounds__(kManageThreads) void lim_manage_long_kernel(LimArgs a, LimWs w) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  __shared__ int vslot[kTopK];
+  __shared__ int lds_miss[kTopK];
+  __shared__ uint32_t lds_stab[kLdsSlots];
+  __shared__ uint32_t lds_skey[kLdsSlots];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  // Invalid rows are answered by lim_manage_kernel; short rows are its own.
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || n <= SHORT * kChunk) return;
+  const int64_t cap = a.source_capacity;
+  const float* s = w.scores + static_cast<int64_t>(b) * cap;
+  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  const bool lds_tables = c <= kLdsSlots;
+  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kTableStride;
+  int32_t* misses = lds_miss;
+  for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  int eq_run = 0, miss_run = 0;
+  {
+    const SelectOut sel = row_threshold<TRES>(s, n, cap, hist, scratch, bcast, red);
     const bool need_rank = sel.cnt_eq != sel.need_eq;
     // Software-pipelined: the next chunk's raw scores and slots are loaded
     // before this chunk is classified, and converted to keys only when used.
@@ -1637,8 +1672,14 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 mgrid(static_cast<uint32_t>(a.batch)), mblock(kManageThreads);
-  if (Q == 1) {  // one kernel; each request picks its path from its own candidate count
-    launch_kernel(kKernLimManage, lim_manage_kernel<8, 16>, mgrid, mblock, stream, a, w);
+  if (Q == 1) {  // each request takes its path from its own candidate count
+    launch_kernel(kKernLimManage, lim_manage_kernel<8>, mgrid, mblock, stream, a, w);
+    if (a.source_capacity > 8 * kChunk) {  // rows longer than 32768 candidates are possible
+      if (a.source_capacity <= 16 * kChunk)
+        launch_kernel(kKernLimManageLong, lim_manage_long_kernel<8, 16>, mgrid, mblock, stream, a, w);
+      else
+        launch_kernel(kKernLimManageLong, lim_manage_long_kernel<8, 0>, mgrid, mblock, stream, a, w);
+    }
     return hipGetLastError();
   }
   // MTP3: thresholds first, one workgroup per (request, query) score row.

@@ -30,7 +30,8 @@ enum KernelId : int {
   kKernIdxProject = 14,
   kKernIdxRope = 15,
   kKernPersist = 16,
-  kKernCount = 17
+  kKernLimManageLong = 17,
+  kKernCount = 18
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.

@@ -406,6 +406,36 @@ def make_chain_case(
     return ChainCase(tensors, meta)
 
 
+RUNNER_CAPACITY = 65536  # default max_model_len (nanovllm/config.py:68), in tokens
+
+
+def caller_layout(t: dict, capacity: int = RUNNER_CAPACITY, pad: int = 0) -> dict:
+    """The same step with the model runner's table layout: index, DRAM and
+    HBM block tables padded to ``capacity``/128 columns with ``pad`` (the
+    runner pads with 0, nanovllm/engine/model_runner.py:747-752; columns past
+    a request's blocks that held -1 get ``pad`` too) and the slot pool
+    ``capacity`` wide (model_runner.py:587-598); new pool columns of a
+    request's row hold -1, of other rows -777.  Works on CPU or GPU tensors;
+    returns a new dict with new tensors for the widened ones."""
+    out = dict(t)
+    cols = capacity // BLOCK
+    for name in ("index_block_table", "dram_block_table", "hbm_block_table"):
+        old = t[name]
+        if old.shape[1] > cols:
+            raise ValueError(f"{name} is wider than {capacity} tokens")
+        new = torch.full((old.shape[0], cols), pad, dtype=old.dtype, device=old.device)
+        keep = old.clone()
+        keep[keep < 0] = pad
+        new[:, :old.shape[1]] = keep
+        out[name] = new
+    pool = t["cache_slots_pool"]
+    wide = torch.full((pool.shape[0], capacity), -777, dtype=pool.dtype, device=pool.device)
+    wide[:, :pool.shape[1]] = pool
+    wide[t["req_pool_entries"].long(), pool.shape[1]:] = -1
+    out["cache_slots_pool"] = wide
+    return out
+
+
 def baseline_config(index: int, seed: int = 0, dtype: torch.dtype = torch.bfloat16, guard: bool = False,
                     source_capacity: int | None = None, table_pad: int = -1, fast_fill: bool = True) -> ChainCase:
     """The configurations of BASELINE.json ``configs`` (0..3) at full size.

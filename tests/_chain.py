@@ -89,28 +89,10 @@ def oracle_chain(case, lim, mtp: bool):
 
 
 def widen_layout(t: dict, capacity: int, pad: int = 0) -> dict:
-    """The same step with the model runner's table layout: index, DRAM and
-    HBM block tables padded to ``capacity``/128 columns with ``pad`` (the
-    runner pads with 0, nanovllm/engine/model_runner.py:747-752) and the slot
-    pool ``capacity`` wide (model_runner.py:587-598); new pool columns of a
-    request's row hold -1, of other rows -777.  Works on CPU or GPU tensors
-    (returns new tensors for the widened ones)."""
-    out = dict(t)
-    cols = capacity // 128
-    for name in ("index_block_table", "dram_block_table", "hbm_block_table"):
-        old = t[name]
-        new = torch.full((old.shape[0], cols), pad, dtype=old.dtype, device=old.device)
-        keep = old.clone()
-        keep[keep < 0] = pad
-        new[:, :old.shape[1]] = keep
-        out[name] = new
-    pool = t["cache_slots_pool"]
-    wide = torch.full((pool.shape[0], capacity), -777, dtype=pool.dtype, device=pool.device)
-    wide[:, :pool.shape[1]] = pool
-    entries = t["req_pool_entries"].long()
-    wide[entries, pool.shape[1]:] = -1
-    out["cache_slots_pool"] = wide
-    return out
+    """The model runner's table layout (nanovllm_amd.workloads.caller_layout)."""
+    from nanovllm_amd.workloads import caller_layout
+
+    return caller_layout(t, capacity, pad)
 
 
 def poison_outputs(t: dict, mtp: bool) -> None:
