@@ -74,7 +74,7 @@ def parse_args():
     p.add_argument("--no-rows", action="store_true",
                    help="skip the per-row measurements (BASELINE configs[2]-[4], LIDU init, indexer "
                         "projection, prefill persist)")
-    p.add_argument("--cpu-steps", type=int, default=8, help="layer-steps of the CPU oracle sample")
+    p.add_argument("--cpu-steps", type=int, default=8, help="layer-steps of the CPU baseline sample")
     p.add_argument("--row", choices=ROW_NAMES, default=None,
                    help="measure one row alone, print its JSON object and exit (for per-row profiles)")
     p.add_argument("--kernels-only", choices=("lim", "fused", "split", "sfa", "copy"), default=None,
@@ -1051,54 +1051,67 @@ def measure_persist(torch, dev, seed: int, reps: int = 5):
 
 
 def cpu_baseline(case, queries_cpu, steps: int):
-    """Time the CPU oracle chain (LIM -> fused copy + attention) on the same
-    inputs: ``steps`` full cfg1 layer-steps on the host cores."""
+    """The layer-step on the host cores: oracle/torch_chain.py, the
+    vectorised PyTorch-CPU chain (batched fp32 products for the scores and
+    the attention, torch.topk, sorts and scatters for the slot bookkeeping,
+    one indexed copy for the misses), on the same cfg1 inputs and the same
+    alternating queries as the GPU steps.  Median of ``steps`` layer-steps
+    after one warmup, on min(16, os.cpu_count()) threads (the box's CPU
+    share).  The numpy oracle (the tests' checker, per-request loops) is
+    timed for two steps beside it."""
     import numpy as np
     import torch
 
     from oracle import dsa_oracle as O
+    from oracle import torch_chain as TC
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = 1
-    t = case.tensors
-    b16 = lambda x: x.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
-    i32 = lambda x: x.numpy().copy()  # noqa: E731
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    t = {k: v.clone() for k, v in case.tensors.items()}
     B = case.meta["batch"]
-    w = b16(t["index_weights"])
-    kc = b16(t["index_key_cache"])
-    table = i32(t["index_block_table"])
-    ncand, ncache, entries = i32(t["num_candidate_tokens"]), i32(t["num_cache_tokens"]), i32(t["req_pool_entries"])
-    pool = i32(t["cache_slots_pool"])
-    qr, qn = b16(t["query_rope"]), b16(t["query"])
-    seq_kv, htab, dtab = i32(t["actual_seq_lengths_kv"]), i32(t["hbm_block_table"]), i32(t["dram_block_table"])
-    hkpe, hckv = b16(t["hbm_k_rope"]).copy(), b16(t["hbm_kv_cache"]).copy()
-    dkpe, dckv = b16(t["dram_k_rope"]), b16(t["dram_kv_cache"])
-    qs = [b16(q) for q in queries_cpu]
-    src = np.zeros((B, 1, 2048), np.int32)
-    dst = np.zeros((B, 1, 2048), np.int32)
-    mc = np.zeros(B, np.int32)
+    scale = case.meta["scale"]
     times = []
     for i in range(steps + 1):
         t0 = time.perf_counter()
-        O.fused_li_manage(qs[i % 2], w, kc, table, ncand, ncache, entries, pool, src, dst, mc)
-        O.fused_copy_sfa(qr, qn, seq_kv, ncache, dst, src.reshape(B, -1), mc, htab, dtab, hkpe, hckv, dkpe, dckv,
-                         case.meta["scale"])
+        TC.fused_li_manage(queries_cpu[i % 2], t["index_weights"], t["index_key_cache"], t["index_block_table"],
+                           t["num_candidate_tokens"], t["num_cache_tokens"], t["req_pool_entries"],
+                           t["cache_slots_pool"], t["topk_src_ids"], t["topk_dst_slots"], t["miss_counts"])
+        TC.fused_copy_sfa(t["query_rope"], t["query"], t["actual_seq_lengths_kv"], t["num_cache_tokens"],
+                          t["topk_dst_slots"], t["topk_src_ids"].view(B, -1), t["miss_counts"], t["hbm_block_table"],
+                          t["dram_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"], t["dram_k_rope"],
+                          t["dram_kv_cache"], scale, t["attention_out"])
         times.append(time.perf_counter() - t0)
-        log(f"bench: cpu oracle step {i}: {times[-1]:.2f}s misses={int(mc.sum())}")
+        log(f"bench: cpu torch chain step {i}: {times[-1] * 1e3:.1f} ms misses={int(t['miss_counts'].sum())}")
     med = float(np.median(times[1:]))
+    # the numpy oracle, two steps on fresh state
+    b16 = lambda x: x.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    i32 = lambda x: x.numpy().copy()  # noqa: E731
+    u = case.tensors
+    pool = i32(u["cache_slots_pool"])
+    hkpe, hckv = b16(u["hbm_k_rope"]).copy(), b16(u["hbm_kv_cache"]).copy()
+    src = np.zeros((B, 1, 2048), np.int32)
+    dst = np.zeros((B, 1, 2048), np.int32)
+    mc = np.zeros(B, np.int32)
+    otimes = []
+    for i in range(2):
+        t0 = time.perf_counter()
+        O.fused_li_manage(b16(queries_cpu[i % 2]), b16(u["index_weights"]), b16(u["index_key_cache"]),
+                          i32(u["index_block_table"]), i32(u["num_candidate_tokens"]), i32(u["num_cache_tokens"]),
+                          i32(u["req_pool_entries"]), pool, src, dst, mc)
+        O.fused_copy_sfa(b16(u["query_rope"]), b16(u["query"]), i32(u["actual_seq_lengths_kv"]),
+                         i32(u["num_cache_tokens"]), dst, src.reshape(B, -1), mc, i32(u["hbm_block_table"]),
+                         i32(u["dram_block_table"]), hkpe, hckv, b16(u["dram_k_rope"]), b16(u["dram_kv_cache"]), scale)
+        otimes.append(time.perf_counter() - t0)
     return {
         "value": round(med * 1e6, 1),
         "unit": "us",
-        "cores": int(threads),
+        "cores": threads,
         "kind": "port",
-        "sample": f"median of {steps} full cfg1 layer-steps (24 requests, LIM + fused copy/attention) of the "
-                  f"numpy oracle after 1 warmup, same inputs; BLAS threads={threads}, os.cpu_count={os.cpu_count()}",
+        "sample": f"median of {steps} full cfg1 layer-steps (24 requests x 32768 candidates: LIM + copy + attention) "
+                  f"of oracle/torch_chain.py (vectorised PyTorch-CPU, fp32) after 1 warmup, same inputs and "
+                  f"alternating queries as the GPU steps; torch threads={threads}, os.cpu_count={os.cpu_count()}",
+        "numpy_oracle_us": round(float(np.mean(otimes)) * 1e6, 1),
     }
-
 
 ROW_FUNCS = {
     "cfg0_bs1": measure_cfg0,
