@@ -302,41 +302,65 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     win_dst[tid] = dst;
     win_flag[tid] = flag;
   };
-  // Chunk c of the tile (c = j * 256 + tid, 72 chunks of 16 bytes per key):
-  // consecutive lanes read consecutive 16 bytes of one row, so a wave reads
-  // whole 1 KiB CKV rows (full-width PCIe requests for host rows).
-  auto load_tile = [&](int w, uint4 (&pf)[kChunksPerThread]) {
-    int t = tid;
-    asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
+  // Two mappings of a tile's 32 x 72 chunks of 16 bytes onto the threads;
+  // both fill the same row-major LDS tile.
+  // * HBM tiles: thread t owns key lk = t >> 3 and its chunks lg + 8j,
+  //   lg = t & 7 (j < 8: CKV bytes [16 lg + 128 j, +16); j = 8: KPE bytes
+  //   [16 lg, +16)): one window lookup per thread and tile and immediate
+  //   offsets for the nine loads.
+  // * The fused kernel (host-sourced rows): chunk c = j * 256 + t, so a wave
+  //   instruction reads one whole 1 KiB CKV row, the request shape the host
+  //   link serves fastest.
+  const int lk = tid >> 3;
+  const int lg = tid & 7;
+  auto load_tile = [&](int w, bool host_tile, uint4 (&pf)[kChunksPerThread]) {
+    if (FUSED && host_tile) {
+      int t = tid;
+      asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
-    for (int jj = 0; jj < kChunksPerThread; ++jj) {
-      const int cidx = jj * kAttnThreads + t;
-      const int k = cidx / kChunksPerKey;
-      const int pc = cidx - k * kChunksPerKey;
-      const int wk = w * kTileKeys + k;
-      const int flag = win_flag[wk];
-      const int64_t src = win_src[wk];
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (flag & 4) {
-        const uint4* base = (FUSED && (flag & 2)) ? (pc < 64 ? dram_ckv + src * 64 : dram_kpe + src * 8)
-                                                  : (pc < 64 ? hbm_ckv + src * 64 : hbm_kpe + src * 8);
-        v = base[pc < 64 ? pc : pc - 64];
+      for (int jj = 0; jj < kChunksPerThread; ++jj) {
+        const int cidx = jj * kAttnThreads + t;
+        const int k = cidx / kChunksPerKey;
+        const int pc = cidx - k * kChunksPerKey;
+        const int wk = w * kTileKeys + k;
+        const int flag = win_flag[wk];
+        const int64_t src = win_src[wk];
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (flag & 4) {
+          const uint4* base = (flag & 2) ? (pc < 64 ? dram_ckv + src * 64 : dram_kpe + src * 8)
+                                         : (pc < 64 ? hbm_ckv + src * 64 : hbm_kpe + src * 8);
+          v = base[pc < 64 ? pc : pc - 64];
+        }
+        pf[jj] = v;
       }
-      pf[jj] = v;
+      return;
+    }
+    const int wk = w * kTileKeys + lk;
+    const int flag = win_flag[wk];
+    const int64_t src = win_src[wk];
+    const uint4* ckv = hbm_ckv + src * 64 + lg;
+    const uint4* kpe = hbm_kpe + src * 8 + lg;
+    if (flag & 4) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[j] = ckv[8 * j];
+      pf[8] = kpe[0];
+    } else {
+#pragma unroll
+      for (int j = 0; j < kChunksPerThread; ++j) pf[j] = make_uint4(0, 0, 0, 0);
     }
   };
-  auto store_tile = [&](int w, const uint4 (&pf)[kChunksPerThread]) {
-    int t = tid;
-    asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
+  auto store_tile = [&](int w, bool host_tile, const uint4 (&pf)[kChunksPerThread]) {
+    if (FUSED && host_tile) {
+      int t = tid;
+      asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
-    for (int jj = 0; jj < kChunksPerThread; ++jj) {
-      const int cidx = jj * kAttnThreads + t;
-      const int k = cidx / kChunksPerKey;
-      const int pc = cidx - k * kChunksPerKey;
-      *reinterpret_cast<uint4*>(&ks[k * kKStride + pc * 8]) = pf[jj];
-      if (FUSED) {
+      for (int jj = 0; jj < kChunksPerThread; ++jj) {
+        const int cidx = jj * kAttnThreads + t;
+        const int k = cidx / kChunksPerKey;
+        const int pc = cidx - k * kChunksPerKey;
+        *reinterpret_cast<uint4*>(&ks[k * kKStride + pc * 8]) = pf[jj];
         const int wk = w * kTileKeys + k;
-        if (win_flag[wk] & 2) {
+        if (win_flag[wk] & 2) {  // a host-sourced miss: persist it to its HBM slot
           const int64_t dst = win_dst[wk];
           if (pc < 64)
             static_cast<uint4*>(a.hbm_ckv)[dst * 64 + pc] = pf[jj];
@@ -344,15 +368,24 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
             static_cast<uint4*>(a.hbm_kpe)[dst * 8 + (pc - 64)] = pf[jj];
         }
       }
+      return;
     }
+    uint16_t* rowp = &ks[lk * kKStride + lg * 8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4*>(rowp + 64 * j) = pf[j];
+    *reinterpret_cast<uint4*>(rowp + kCkvDim) = pf[8];
   };
 
   // The first tile's loads (possibly host rows) are issued before the
   // query loads.
+  // The fused kernel reads every tile row per wave: with the key-per-8-lanes
+  // mapping on its HBM tiles, the host link under them served the miss tiles
+  // more slowly (cfg1 fused kernel 129 -> 138 us).
+  auto is_host_tile = [&](int, int) { return FUSED; };
   uint4 pf[kChunksPerThread];
   resolve_window(0);
   __syncthreads();
-  load_tile(0, pf);
+  load_tile(0, is_host_tile(0, 0), pf);
   load_queries();
 
   const float qscale = a.scale * kLog2e;
@@ -366,13 +399,13 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     if (first > 0) {
       resolve_window(first);
       __syncthreads();
-      load_tile(0, pf);
+      load_tile(0, is_host_tile(first, 0), pf);
     }
     const int wtiles = min(kWindowTiles, my_tiles - first);
     for (int w = 0; w < wtiles; ++w) {
-      store_tile(w, pf);
+      store_tile(w, is_host_tile(first, w), pf);
       __syncthreads();                     // tile w resident in LDS
-      if (w + 1 < wtiles) load_tile(w + 1, pf);  // in flight during the MFMA work below
+      if (w + 1 < wtiles) load_tile(w + 1, is_host_tile(first, w + 1), pf);  // in flight during the MFMA work below
 
       if (wave_active && plan.active) {
         // S^T tile: two 16-key blocks; lane holds S[head][kt*16 + 4g + i].
@@ -430,7 +463,10 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
             }
           }
           // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
-          // ~16 mantissa bits of P instead of 8.
+          // ~16 mantissa bits of P instead of 8.  (One rounded P is not
+          // enough: with near-uniform attention over thousands of keys the
+          // output is a small mean of zero-mean rows, and P's rounding error
+          // does not shrink with it.)
           typename T::vec8 pb_hi, pb_lo;
           uint16_t* phs = reinterpret_cast<uint16_t*>(&pb_hi);
           uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
