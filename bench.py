@@ -859,10 +859,10 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
             step(i)
             misses.append(int(runner.owner_outputs(0, B)["miss_counts"].sum()))
     torch.cuda.synchronize()
-    names = ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel", "sfa_split_kernel_fused",
-             "sfa_combine_kernel")
-    km = _kernel_means(kt, names)
-    per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names}
+    names = ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel", "lim_threshold_kernel",
+             "lim_long_pass_a_kernel", "lim_long_pass_b_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel")
+    km = {k: v for k, v in _kernel_means(kt, names).items() if v == v}  # kernels this step ran
+    per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names if n in km}
     graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran
     # Group prefetch: the split path with each group's copies on a side stream
     # once its owner has selected (an even number of steps ran: parity 0).

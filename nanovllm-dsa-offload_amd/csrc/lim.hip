@@ -68,10 +68,21 @@ struct LimWs {
   int32_t* part_counts; // [B, parts, 8] MTP: per chunk, misses by first-selecting query, selected per query
   int32_t* vslot;       // [B, 8192] MTP: victim slots
   int32_t* nvict;       // [B] MTP: victims found
+  int32_t* done;        // [B] chunked MTP0 rows: chunks of pass A finished
 };
 
 // MTP3 management runs one workgroup per kChunk-token chunk of a request.
 __host__ __device__ inline int64_t mtp_parts(int64_t cap) { return (cap + 4095) / 4096; }
+
+// MTP0 rows longer than kShortRows * 4096 candidates leave the register
+// kernel.  At batches up to kChunkedRows they run chunked (one workgroup per
+// 4096-token chunk, like MTP3); larger batches keep one workgroup per row,
+// which already spreads over as many CUs.
+constexpr int kShortRes = 8;
+constexpr int64_t kChunkedRows = 16;
+__host__ __device__ inline bool chunked_long(int64_t batch, int64_t cap, int queries) {
+  return queries == 1 && batch <= kChunkedRows && cap > kShortRes * 4096;
+}
 
 LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
   char* p = static_cast<char*>(base);
@@ -87,15 +98,19 @@ LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
   w.select = reinterpret_cast<uint32_t*>(p);
   p += align256(sizeof(uint32_t) * 4 * batch * queries);
   w.masks = nullptr;
-  w.part_counts = w.vslot = w.nvict = nullptr;
+  w.part_counts = w.vslot = w.nvict = w.done = nullptr;
   if (queries > 1) {
     w.masks = reinterpret_cast<uint8_t*>(p);
     p += align256(static_cast<size_t>(batch) * cap);
+  }
+  if (queries > 1 || chunked_long(batch, cap, queries)) {
     w.part_counts = reinterpret_cast<int32_t*>(p);
     p += align256(sizeof(int32_t) * batch * mtp_parts(cap) * 8);
     w.vslot = reinterpret_cast<int32_t*>(p);
     p += align256(sizeof(int32_t) * batch * kUnionCap);
     w.nvict = reinterpret_cast<int32_t*>(p);
+    p += align256(sizeof(int32_t) * batch);
+    w.done = reinterpret_cast<int32_t*>(p);
   }
   return w;
 }
@@ -813,7 +828,7 @@ __device__ __forceinline__ SelectOut row_threshold(const float* s, int n, int64_
 // workspace for the MTP3 management kernels.  One workgroup per row; RES > 0
 // keeps the row's keys in registers (RES chunks of 4096 tokens).
 template <int RES>
-__global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a, LimWs w, int queries) {
+__global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a, LimWs w, int queries, int min_n) {
   __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
@@ -826,7 +841,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
   const int r = a.pool_entries[b];
   const bool valid = queries > 1 ? lim_mtp_row_valid(n, c, r, a.source_capacity, a.pool_rows)
                                  : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
-  if (!valid) return;
+  if (!valid || n < min_n) return;
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + (static_cast<int64_t>(b) * queries + q) * cap;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
@@ -860,10 +875,12 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
     out[2] = static_cast<uint32_t>(sel.cnt_eq);
     out[3] = static_cast<uint32_t>(cutoff);
   }
-  // MTP3: the request's slot table starts all-free for the chunked passes.
-  if (queries > 1 && q == 0) {
+  // The chunked passes (MTP3, long MTP0 rows) start from an all-free slot
+  // table and, for MTP0, a zero count of finished chunks.
+  if (q == 0) {
     uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
     for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
+    if (queries == 1 && tid == 0) w.done[b] = 0;
   }
 }
 
@@ -931,6 +948,9 @@ __device__ inline void load_pool8(const int32_t* pool, int n, int t0, int32_t* s
   }
 }
 
+__device__ __forceinline__ void write_hit_rows(const LimArgs& a, int b, int c, int m, const uint32_t* stab,
+                                               int* scratch);
+
 // Victims, pairing, pool update and the output row of one MTP0 request.
 __device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int m, int32_t* pool, uint32_t* stab, uint32_t* skey,
                             const int32_t* misses, int* vslot, uint32_t* hist, int* scratch, int* bcast,
@@ -953,7 +973,19 @@ __device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int 
       pool[t] = d;
     }
   }
-  // Hits by descending old slot: position p of the descending scan is slot c-1-p.
+  write_hit_rows(a, b, c, m, stab, scratch);
+}
+
+// The hit half of an MTP0 output row: positions m, m+1, ... get the hits by
+// descending old slot (reference BuildHitMissKey order), the positions a
+// corrupt pool (duplicate slots) leaves unfilled get -1, and miss_counts[b]
+// = m.
+__device__ __forceinline__ void write_hit_rows(const LimArgs& a, int b, int c, int m, const uint32_t* stab,
+                                               int* scratch) {
+  const int tid = threadIdx.x;
+  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
+  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
+  // Position p of the descending scan is slot c-1-p.
   int hit_run = 0;
   for (int base = 0; base < c; base += kSlotChunk) {
     const int p0 = base + tid * kSlotItems;
@@ -1237,6 +1269,165 @@ __global__ __launch_bounds__(kManageThreads) void lim_manage_long_kernel(LimArgs
   }
   __syncthreads();
   mtp0_finish(a, b, c, miss_run, pool, stab, skey, misses, vslot, hist, scratch, bcast, red);
+}
+
+// Long MTP0 rows (more than kShortRes * kChunk candidates) at batches up to
+// kChunkedRows, one workgroup per 4096-token chunk of a request, after
+// lim_threshold_kernel (threshold key and tie cutoff per row, slot table
+// reset, finished-chunk count zeroed):
+//   pass A   each chunk classifies its tokens (selected: key above the
+//            threshold, or equal with token <= cutoff), records cached tokens
+//            in the slot table and counts its misses; the last chunk of the
+//            request to finish (a device-scope counter, no waiting) selects
+//            the victims and writes the hit half of the output row;
+//   pass B   each chunk writes its misses after those of the chunks before
+//            it, paired with the ascending victim slots, and updates the pool.
+// Pass B reads pool entries only of selected tokens: evictions rewrite
+// entries of unselected tokens only, and a miss's entry only its own chunk.
+__device__ inline bool mtp0_selected(uint32_t key, int t, uint32_t thr, int cutoff) {
+  return key > thr || (key == thr && t <= cutoff);
+}
+
+__global__ __launch_bounds__(kManageThreads) void lim_long_pass_a_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  __shared__ int last;
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || n <= kShortRes * kChunk) return;
+  const int64_t cap = a.source_capacity;
+  int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
+  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
+  int my_miss = 0;
+  if (part * kChunk < n) {
+    const uint32_t* sel = w.select + static_cast<int64_t>(b) * 4;
+    const uint32_t thr = sel[0];
+    const int cutoff = static_cast<int>(sel[3]);
+    const float* s = w.scores + static_cast<int64_t>(b) * cap;
+    const int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+    const int t0 = part * kChunk + tid * kItems;
+    uint32_t u[kItems];
+    int32_t slot[kItems];
+    bool in[kItems];
+    load_tokens8(s, pool, n, t0, u, slot, in);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      if (!in[e]) continue;
+      const int t = t0 + e;
+      const bool selected = mtp0_selected(u[e], t, thr, cutoff);
+      if (slot[e] >= 0 && slot[e] < c) {
+        if (selected) {
+          stab[slot[e]] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
+        } else {
+          stab[slot[e]] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
+          skey[slot[e]] = u[e];
+        }
+      } else if (selected) {
+        ++my_miss;
+      }
+    }
+  }
+  const int chunk_misses = block_sum(my_miss, scratch);
+  if (tid == 0) counts[part * 8] = chunk_misses;
+  // The barrier waits for every wave's stores; one release fence then makes
+  // them visible device-wide before the arrival count, and the last chunk of
+  // the request to arrive acquires the others' (one agent-scope fence each
+  // way: a full fence per wave writes back and invalidates the XCD's L2
+  // under the other chunks' feet).
+  __syncthreads();
+  if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    last = atomicAdd(&w.done[b], 1) == parts - 1 ? 1 : 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (!last) return;
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  int local = 0;
+  for (int p = tid; p < parts; p += kManageThreads) local += counts[p * 8];
+  const int m = block_sum(local, scratch);  // also orders the hist clearing before the selects
+  int32_t* vslot = w.vslot + static_cast<int64_t>(b) * kUnionCap;
+  const int nv = c <= 4 * kManageThreads    ? select_victims_regs<4>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
+                 : c <= 16 * kManageThreads ? select_victims_regs<16>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
+                                            : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
+  if (tid == 0) w.nvict[b] = nv;
+  write_hit_rows(a, b, c, m, stab, scratch);
+}
+
+__global__ __launch_bounds__(kManageThreads) void lim_long_pass_b_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || n <= kShortRes * kChunk) return;
+  if (part * kChunk >= n) return;
+  const int64_t cap = a.source_capacity;
+  const int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
+  int local = 0;
+  for (int p = tid; p < part; p += kManageThreads) local += counts[p * 8];
+  const int before = block_sum(local, scratch);  // misses of the chunks before this one
+  const uint32_t* sel = w.select + static_cast<int64_t>(b) * 4;
+  const uint32_t thr = sel[0];
+  const int cutoff = static_cast<int>(sel[3]);
+  const int nv = w.nvict[b];
+  const int32_t* vslot = w.vslot + static_cast<int64_t>(b) * kUnionCap;
+  const uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  const float* s = w.scores + static_cast<int64_t>(b) * cap;
+  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
+  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
+  const int t0 = part * kChunk + tid * kItems;
+  uint32_t u[kItems];
+  bool in[kItems];
+  if (t0 + kItems <= n) {
+    const float4 x = *reinterpret_cast<const float4*>(s + t0);
+    const float4 y = *reinterpret_cast<const float4*>(s + t0 + 4);
+    u[0] = score_key(x.x); u[1] = score_key(x.y); u[2] = score_key(x.z); u[3] = score_key(x.w);
+    u[4] = score_key(y.x); u[5] = score_key(y.y); u[6] = score_key(y.z); u[7] = score_key(y.w);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) in[e] = true;
+  } else {
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      in[e] = t0 + e < n;
+      u[e] = in[e] ? score_key(s[t0 + e]) : 0u;
+    }
+  }
+  unsigned missm = 0u;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    if (!in[e] || !mtp0_selected(u[e], t0 + e, thr, cutoff)) continue;
+    const int32_t slot = pool[t0 + e];  // a selected token: no other chunk writes its entry
+    if (!(slot >= 0 && slot < c)) missm |= 1u << e;
+  }
+  int tot;
+  int pos = before + block_exclusive_scan(__popc(missm), scratch, &tot);
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    if (!((missm >> e) & 1u)) continue;
+    const int t = t0 + e;
+    const int d = pos < nv ? vslot[pos] : -1;
+    if (pos < kTopK) {
+      out_src[pos] = t;
+      out_dst[pos] = d;
+    }
+    if (d >= 0) {
+      const uint32_t ent = stab[d];
+      if ((ent >> kStateShift) == kStateCand) pool[ent & kTokenMask] = -1;  // an unselected token
+      pool[t] = d;
+    }
+    ++pos;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1672,28 +1863,34 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 mgrid(static_cast<uint32_t>(a.batch)), mblock(kManageThreads);
+  const dim3 tgrid(static_cast<uint32_t>(a.batch * Q));
+  const int parts = static_cast<int>(mtp_parts(a.source_capacity));
+  if (parts > kManageThreads) return hipErrorInvalidValue;  // MTP3 pass B scans one part per thread
+  const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
+  auto launch_threshold = [&](int min_n) {
+    if (a.source_capacity <= 16 * kChunk)
+      launch_kernel(kKernLimThreshold, lim_threshold_kernel<16>, tgrid, mblock, stream, a, w, Q, min_n);
+    else
+      launch_kernel(kKernLimThreshold, lim_threshold_kernel<0>, tgrid, mblock, stream, a, w, Q, min_n);
+  };
   if (Q == 1) {  // each request takes its path from its own candidate count
-    launch_kernel(kKernLimManage, lim_manage_kernel<8>, mgrid, mblock, stream, a, w);
-    if (a.source_capacity > 8 * kChunk) {  // rows longer than 32768 candidates are possible
-      if (a.source_capacity <= 16 * kChunk)
-        launch_kernel(kKernLimManageLong, lim_manage_long_kernel<8, 16>, mgrid, mblock, stream, a, w);
-      else
-        launch_kernel(kKernLimManageLong, lim_manage_long_kernel<8, 0>, mgrid, mblock, stream, a, w);
+    launch_kernel(kKernLimManage, lim_manage_kernel<kShortRes>, mgrid, mblock, stream, a, w);
+    if (a.source_capacity <= kShortRes * kChunk) return hipGetLastError();  // no row can be longer
+    if (chunked_long(a.batch, a.source_capacity, Q)) {
+      launch_threshold(kShortRes * kChunk + 1);
+      launch_kernel(kKernLimLongPassA, lim_long_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
+      launch_kernel(kKernLimLongPassB, lim_long_pass_b_kernel, pgrid, mblock, stream, a, w, parts);
+    } else if (a.source_capacity <= 16 * kChunk) {
+      launch_kernel(kKernLimManageLong, lim_manage_long_kernel<kShortRes, 16>, mgrid, mblock, stream, a, w);
+    } else {
+      launch_kernel(kKernLimManageLong, lim_manage_long_kernel<kShortRes, 0>, mgrid, mblock, stream, a, w);
     }
     return hipGetLastError();
   }
   // MTP3: thresholds first, one workgroup per (request, query) score row.
-  const dim3 tgrid(static_cast<uint32_t>(a.batch * Q));
-  if (a.source_capacity <= 16 * kChunk) {
-    launch_kernel(kKernLimThreshold, lim_threshold_kernel<16>, tgrid, mblock, stream, a, w, Q);
-  } else {
-    launch_kernel(kKernLimThreshold, lim_threshold_kernel<0>, tgrid, mblock, stream, a, w, Q);
-  }
+  launch_threshold(0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int parts = static_cast<int>(mtp_parts(a.source_capacity));
-  if (parts > kManageThreads) return hipErrorInvalidValue;  // pass B scans one part per thread
-  const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
   launch_kernel(kKernLimMtpPassA, lim_mtp_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
   launch_kernel(kKernLimMtpVictims, lim_mtp_victims_kernel, mgrid, mblock, stream, a, w, parts);
   launch_kernel(kKernLimMtpPassB, lim_mtp_pass_b_kernel, pgrid, mblock, stream, a, w, parts);
@@ -1707,11 +1904,11 @@ size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries) 
   total += 2 * align256(sizeof(uint32_t) * batch * kTableStride);
   total += align256(sizeof(int32_t) * batch * kUnionCap);
   total += align256(sizeof(uint32_t) * 4 * batch * queries);
-  if (queries > 1) {
-    total += align256(static_cast<size_t>(batch) * source_capacity);
+  if (queries > 1) total += align256(static_cast<size_t>(batch) * source_capacity);
+  if (queries > 1 || chunked_long(batch, source_capacity, queries)) {
     total += align256(sizeof(int32_t) * batch * mtp_parts(source_capacity) * 8);
     total += align256(sizeof(int32_t) * batch * kUnionCap);
-    total += align256(sizeof(int32_t) * batch);
+    total += 2 * align256(sizeof(int32_t) * batch);
   }
   return total;
 }

@@ -170,7 +170,7 @@ def test_lim_mtp_bit_exact(heads):
     assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
 
 
-def _tie_case(mtp: bool, positives, seed=11):
+def _tie_case(mtp: bool, positives, seed=11, n_tokens=12288):
     """Scores with exact ties at the top-2048 threshold: query row j of a
     request reads key dim j only, and key dim j is positive for `positives[j]`
     tokens of the request (values 1 + m/128, exact in 16 bits), zero
@@ -178,7 +178,7 @@ def _tie_case(mtp: bool, positives, seed=11):
     2048th score is a 0 shared by thousands of tokens (lowest tokens win)."""
     from nanovllm_amd.workloads import make_chain_case
 
-    B, N = 3, 12288
+    B, N = 3, n_tokens
     case = make_chain_case(B, N, [8192, 8704, 10240] if mtp else [2048, 4096, 6144], [4, 20, 60], seed=seed,
                            mtp=mtp, guard=False)
     t = case.tensors
@@ -204,10 +204,14 @@ def _tie_case(mtp: bool, positives, seed=11):
     return case
 
 
-@pytest.mark.parametrize("mtp,positives", [(False, [700]), (True, [500, 900, 1300, 1900])])
-def test_lim_ties_at_threshold_bit_exact(mtp, positives):
-    case = _tie_case(mtp, positives)
-    print(f"LIM ties mtp={mtp} positives={positives}", flush=True)
+# 40960-token rows take the chunked path for long rows (batch <= 16).
+TIE_CASES = [(False, [700], 12288), (False, [700], 40960), (True, [500, 900, 1300, 1900], 12288)]
+
+
+@pytest.mark.parametrize("mtp,positives,n_tokens", TIE_CASES)
+def test_lim_ties_at_threshold_bit_exact(mtp, positives, n_tokens):
+    case = _tie_case(mtp, positives, n_tokens=n_tokens)
+    print(f"LIM ties mtp={mtp} positives={positives} N={n_tokens}", flush=True)
     expect = oracle_lim(case, mtp=mtp)
     d = case.to_device("cuda", host_mapped=False)
     _run_lim(d, mtp=mtp)
@@ -227,15 +231,15 @@ def _assert_matches(d, expect, mtp):
     assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
 
 
-@pytest.mark.parametrize("mtp,positives", [(False, [700]), (True, [500, 900, 1300, 1900])])
-def test_lim_unmapped_index_blocks_score_lowest(mtp, positives):
+@pytest.mark.parametrize("mtp,positives,n_tokens", TIE_CASES)
+def test_lim_unmapped_index_blocks_score_lowest(mtp, positives, n_tokens):
     """Index block-table entries that name no key block (-1, or at or past
     the cache's block count) score -FLT_MAX: below every real score, above
     a free slot when victims are ranked.  The reference reads such an
     entry's memory unchecked (fused_li_manage_service_cube.h:217), so this
     is this library's own guard, restated by the oracle.  One unmapped block
     in the zero-score tie region (block 0), others above it."""
-    case = _tie_case(mtp, positives)
+    case = _tie_case(mtp, positives, n_tokens=n_tokens)
     t = case.tensors
     table = t["index_block_table"]
     nblk = t["index_key_cache"].shape[0]
@@ -248,6 +252,28 @@ def test_lim_unmapped_index_blocks_score_lowest(mtp, positives):
     d = case.to_device("cuda", host_mapped=False)
     _run_lim(d, mtp=mtp)
     _assert_matches(d, expect, mtp)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_lim_long_rows_small_batch_bit_exact(dtype):
+    """Rows past 32768 candidates at a small batch run chunked (a workgroup
+    per 4096 tokens, the last chunk to finish picking the victims): long rows
+    with C = 2048, 6144 and 12288 (the three victim selects) beside a short
+    row with its slot tables in the workspace; every output and the pool
+    bit-exact, and the repeat call has no misses."""
+    from nanovllm_amd.workloads import make_chain_case
+
+    case = make_chain_case(4, [40960, 65536, 20480, 49152], [2048, 6144, 12288, 12288], [3, 64, 127, 9], seed=23,
+                           dtype=dtype, fast_fill=True)
+    print(f"LIM long rows {dtype} halvings={case.meta['halvings']} miss={case.meta['miss_target']}", flush=True)
+    expect = oracle_lim(case)
+    assert int(expect["miss_counts"].sum()) > 0
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d)
+    _assert_matches(d, expect, False)
+    _run_lim(d)  # same query again: everything is cached now
+    assert (ints(d["miss_counts"]) == 0).all()
+    assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
 
 
 def test_lim_row_guards():
