@@ -864,6 +864,23 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
     km = {k: v for k, v in _kernel_means(kt, names).items() if v == v}  # kernels this step ran
     per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names if n in km}
     graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran
+    # The split path per layer (scatter_copy then sparse_tail_attention).
+    sp = IndexShareDecodeStep(groups, layers, fused=False)
+
+    def step_sp(i):
+        owner_kw = dict(base, query_index=qs[i % 2], index_weights=t["index_weights"])
+        sp.step(ctx, lambda layer: owner_kw if groups.is_owner(layer) else base)
+
+    for i in range(2):
+        step_sp(i)
+    torch.cuda.synchronize()
+    sp_graph_ms = _graph_step_us(torch, [lambda: step_sp(0), lambda: step_sp(1)], steps) / 1000
+    with _lib.KernelTimer(capacity=256 * steps) as kt_sp:
+        for i in range(steps):
+            step_sp(i)
+    torch.cuda.synchronize()
+    km_sp = {k: v for k, v in _kernel_means(kt_sp, ("scatter_copy_kernel", "sfa_split_kernel", "sfa_combine_kernel"))
+             .items() if v == v}
     # Group prefetch: the split path with each group's copies on a side stream
     # once its owner has selected (an even number of steps ran: parity 0).
     pf = IndexShareDecodeStep(groups, layers, fused=False, prefetch=True)
@@ -889,6 +906,7 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
                        f"{len(groups.shared_layer_idxs)} shared), bs={B}, prompts {N}, C={C}, tails U[1,127], "
                        "misses 5-15%, offload_fuse, one HIP graph per step",
            "step_ms": round(graph_ms, 3), "eager_step_ms": round(eager_ms, 3),
+           "split_step_ms": round(sp_graph_ms, 3), "split_kernels_us": km_sp,
            "prefetch_step_ms": round(pf_graph_ms, 3), "prefetch_eager_step_ms": round(pf_eager_ms, 3),
            "us_per_layer": round(graph_ms * 1000 / L, 2),
            "miss_rows_per_layer": round(miss_rows, 1), "host_link_bytes_per_step": int(copy_bytes),
@@ -898,7 +916,7 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
            "fused_h2d_GBs": round(miss_rows * ROW_BYTES / (km["sfa_split_kernel_fused"] * 1e-6) / 1e9, 2),
            "step_h2d_GBs": round(copy_bytes / (graph_ms * 1e-3) / 1e9, 2),
            "prefetch_step_h2d_GBs": round(copy_bytes / (pf_graph_ms * 1e-3) / 1e9, 2)}
-    del runner, pf, layers, d, t, case
+    del runner, sp, pf, layers, d, t, case
     torch.cuda.empty_cache()
     return out
 

@@ -57,6 +57,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxSlack = 8.f;  // base-2 headroom of the running max (P < 256)
 constexpr int kMissSplits = 2;  // fused: least splits of a row that take its host-sourced tiles
 constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgroups per launch
+constexpr int kFusedMaxSplits = 16;  // fused: most splits per row from kFusedCapRows rows on
+constexpr int kFusedCapRows = 8;
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -633,7 +635,14 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int64_t rows = a.batch * a.rows_per_request;
   if (rows == 0) return hipSuccess;
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
-  const int splits = choose_splits(rows, hgroups);
+  // From kFusedCapRows rows on, the fused kernel lasts as long as its
+  // host-link-bound miss splits, so its HBM splits can take more tiles each:
+  // at most kFusedMaxSplits splits per row keeps the partials (128 KB per
+  // split and row at 64 heads) and their merge small (8 rows: combine 6.9 ->
+  // 4.2 us, the fused kernel unchanged).  With fewer rows the HBM tiles are
+  // the longer path and keep every split (1 row: 64).
+  int splits = choose_splits(rows, hgroups);
+  if (FUSED && rows >= kFusedCapRows && splits > kFusedMaxSplits) splits = kFusedMaxSplits;
   SfaArgs args = a;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
   launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED, kKeysAll>,
