@@ -86,8 +86,10 @@ def parse_args():
 
 
 # ---- hardware-counter helpers ------------------------------------------------
+# The MTP0 management kernels, in launch order (one workgroup per 4096-token chunk).
+MANAGE_KERNELS = ("lim_hist_kernel", "lim_classify_kernel", "lim_place_kernel")
 PMC_KERNELS = ("lim_score_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
-               "lim_threshold_kernel", "lim_manage_kernel", "sfa_split_kernel",
+               "lim_threshold_kernel") + MANAGE_KERNELS + ("sfa_split_kernel",
                "sfa_combine_kernel", "scatter_copy_kernel", "indexer_project_kernel")
 PMC_PROFILE = REPO / "profiles" / "lim_score_cfg1_pmc.txt"
 
@@ -295,7 +297,7 @@ def measure_cfg0(torch, np, dev, seed: int, steps: int = 20):
         with _lib.KernelTimer(capacity=16 * steps) as kt:
             ch.run(kind, steps, miss_log=log_)
         torch.cuda.synchronize()
-        names = ("lim_score_kernel", "lim_manage_kernel") + (
+        names = ("lim_score_kernel",) + MANAGE_KERNELS + (
             ("scatter_copy_kernel", "sfa_split_kernel", "sfa_combine_kernel") if kind == "split"
             else ("sfa_split_kernel_fused", "sfa_combine_kernel"))
         out[f"{kind}_step_us"] = round(ms * 1000, 2)
@@ -340,7 +342,7 @@ def measure_ref_lim(torch, np, dev, seed: int, steps: int = 20):
             ch.lim(0)
     torch.cuda.synchronize()
     n_tokens = 24 * 65536
-    km = _kernel_table(kt, ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel"))
+    km = _kernel_table(kt, ("lim_score_kernel",) + MANAGE_KERNELS)
     out = {"workload": "fused_li_manage alone: bs=24, sources 65536, C=8192, 32 index heads, "
                        "model-runner table layout, pool restored before each HIP-graph replay",
            "step_us": round(us, 2), "kernels_us": km,
@@ -528,8 +530,9 @@ def main() -> int:
     torch.cuda.synchronize()
     del narrow_graphs, narrow, tn
 
-    k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel",
-                                                  "sfa_split_kernel_fused", "sfa_combine_kernel")}
+    k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel",) + MANAGE_KERNELS +
+         ("sfa_split_kernel_fused", "sfa_combine_kernel")}
+    k["lim_manage"] = sum(k[name] for name in MANAGE_KERNELS)
     ks = {name: kt_split.mean_ms(name) for name in ("scatter_copy_kernel", "sfa_split_kernel")}
 
     # ---- roofline of the index-key scan (lim_score_kernel) ------------------
@@ -556,7 +559,7 @@ def main() -> int:
         del d, t, head, case
         torch.cuda.empty_cache()
         rows = {"cfg1": {"lim_score_us": round(k["lim_score_kernel"] * 1000, 2),
-                         "lim_manage_us": round(k["lim_manage_kernel"] * 1000, 2),
+                         "lim_manage_us": round(k["lim_manage"] * 1000, 2),
                          "lim_score_hbm_GBs": round(score_ach, 1),
                          "scatter_copy_us": round(ks["scatter_copy_kernel"] * 1000, 2),
                          "scatter_copy_h2d_GBs": round(scatter_h2d, 2),
@@ -607,11 +610,11 @@ def main() -> int:
             "fuse_graph_step": round(value_us, 2), "fuse_graph_1step": round(graph1_ms * 1000, 2),
             "fuse_eager_step": round(eager_ms * 1000, 2),
             "fuse_graph_step_narrow_tables": round(narrow_ms * 1000, 2),
-            "lim_manage_narrow_tables": round(kt_narrow.mean_ms("lim_manage_kernel") * 1000, 2),
+            "lim_manage_narrow_tables": round(sum(kt_narrow.mean_ms(n) for n in MANAGE_KERNELS) * 1000, 2),
             "split_graph_step": round(split_graph_ms * 1000, 2),
             "split_eager_step": round(split_ms * 1000, 2),
-            "lim_score": round(k["lim_score_kernel"] * 1000, 2), "lim_manage": round(k["lim_manage_kernel"] * 1000, 2),
-            "lim_manage_long_empty": round(k["lim_manage_long_kernel"] * 1000, 2),
+            "lim_score": round(k["lim_score_kernel"] * 1000, 2), "lim_manage": round(k["lim_manage"] * 1000, 2),
+            **{name[:-len("_kernel")]: round(k[name] * 1000, 2) for name in MANAGE_KERNELS},
             "fused_copy_sfa_split": round(k["sfa_split_kernel_fused"] * 1000, 2),
             "sfa_combine": round(k["sfa_combine_kernel"] * 1000, 2),
             "scatter_copy": round(ks["scatter_copy_kernel"] * 1000, 2), "sfa_split": round(ks["sfa_split_kernel"] * 1000, 2),
@@ -772,8 +775,7 @@ def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
             step(i)
             misses.append(int(t["miss_counts"].sum()))
     torch.cuda.synchronize()
-    km = _kernel_means(kt, ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel", "sfa_split_kernel_fused",
-                            "sfa_combine_kernel"))
+    km = _kernel_means(kt, ("lim_score_kernel",) + MANAGE_KERNELS + ("sfa_split_kernel_fused", "sfa_combine_kernel"))
     graph_us = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps)  # parity 0: an even number ran
     n_tokens = int(t["num_candidate_tokens"].sum())
     miss_rows = float(np.mean(misses))
@@ -859,8 +861,7 @@ def measure_cfg4(torch, np, dev, seed: int, steps: int = 6):
             step(i)
             misses.append(int(runner.owner_outputs(0, B)["miss_counts"].sum()))
     torch.cuda.synchronize()
-    names = ("lim_score_kernel", "lim_manage_kernel", "lim_manage_long_kernel", "lim_threshold_kernel",
-             "lim_long_pass_a_kernel", "lim_long_pass_b_kernel", "sfa_split_kernel_fused", "sfa_combine_kernel")
+    names = ("lim_score_kernel",) + MANAGE_KERNELS + ("sfa_split_kernel_fused", "sfa_combine_kernel")
     km = {k: v for k, v in _kernel_means(kt, names).items() if v == v}  # kernels this step ran
     per_step = {n: round(sum(ms for k, ms in kt.records if k == n) / steps * 1000, 1) for n in names if n in km}
     graph_ms = _graph_step_us(torch, [lambda: step(0), lambda: step(1)], steps) / 1000  # parity 0: an even number ran

@@ -1,17 +1,18 @@
 // fused_li_manage / fused_li_manage_mtp: LightningIndexer scores, top-2048
 // selection and persistent HBM-slot bookkeeping on gfx950.
 //
-// Two launches per call:
+// Per call:
 //   1. lim_score_kernel  — one wavefront per 128-token index block.  The
 //      block's key rows are the MFMA B operand (32 tokens x 16 dims per
 //      v_mfma_f32_32x32x16), the request's index query rows the A operand
 //      (staged once per workgroup in LDS), fp32 accumulation, then ReLU,
 //      per-head weight and head reduction in registers.  Scores go to an fp32
 //      workspace row per query; the key scan is the only large HBM stream.
-//   2. lim_manage_kernel(_mtp) — one 512-thread workgroup per request:
-//      radix select of the top-2048 threshold on the scores, one ordered
-//      pass over the candidates against the request's pool row, victim
-//      selection, pairing and pool update.
+//   2. management, chunked: one 512-thread workgroup per 4096-token chunk of
+//      a request — the top-2048 threshold, the ordered pass over the
+//      candidates against the request's pool row, victim selection, pairing
+//      and pool update (MTP0: lim_hist / lim_classify / lim_place; MTP3:
+//      lim_threshold / lim_mtp_pass_a / lim_mtp_victims / lim_mtp_pass_b).
 //
 // Canonical semantics (the reference leaves victim choice and in-row order
 // implementation-defined; these rules make every integer output exact):
@@ -47,9 +48,12 @@ constexpr int kDigitBits = 13;                    // radix digit width
 constexpr int kBins = 1 << kDigitBits;            // radix histogram bins
 constexpr int kBinsPerThread = kBins / kManageThreads;
 constexpr int kGatherKeys = 64;                   // radix select: bins this small are ranked directly
+constexpr int kHistBits = 12;                     // MTP0: first digit of the chunked threshold search
+constexpr int kHistBins = 1 << kHistBits;
+constexpr int kGatherPart = 128;                  // MTP0: in-bin tokens a chunk can hand over
+constexpr int kRankDirect = 512;                  // MTP0: in-bin tokens ranked pairwise by the last chunk
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr int kTableStride = kSlotStride + kManageThreads;  // workspace slot tables: + one junk word per thread
-constexpr int kLdsSlots = 4096;     // MTP0: cache budgets up to this keep their slot tables in LDS
 constexpr uint32_t kStateShift = 24;
 constexpr uint32_t kStateFree = 0;
 constexpr uint32_t kStateHit = 1;
@@ -60,60 +64,55 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 
 struct LimWs {
   float* scores;        // [B*Q, S_cap]
-  uint32_t* slot_table; // [B, 16384] token | state << 24
-  uint32_t* slot_key;   // [B, 16384] score key of candidate slots
-  int32_t* miss_list;   // [B, 8192]
-  uint32_t* select;     // [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq, tie cutoff token (threshold kernel)
-  uint8_t* masks;       // [B, S_cap] per-token query mask (MTP)
-  int32_t* part_counts; // [B, parts, 8] MTP: per chunk, misses by first-selecting query, selected per query
-  int32_t* vslot;       // [B, 8192] MTP: victim slots
-  int32_t* nvict;       // [B] MTP: victims found
-  int32_t* done;        // [B] chunked MTP0 rows: chunks of pass A finished
+  uint32_t* slot_table; // [B, kTableStride] token | state << 24
+  uint32_t* slot_key;   // [B, kTableStride] score key of candidate slots
+  uint32_t* select;     // [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq, tie cutoff token
+  int32_t* part_counts; // [B, parts, 8] per 4096-token chunk: MTP0 misses, in-bin tokens, then the misses before it; MTP3 misses by first-selecting query, selected per query
+  int32_t* vslot;       // MTP0: [B, 2, kTopK] victim slots, then the token each evicts (-1: free); MTP3: [B, 8192] slots
+  int32_t* nvict;       // [B] victims found
+  uint8_t* masks;       // MTP3: [B, S_cap] per-token query mask
+  int32_t* done;        // MTP0: [B] chunks that finished lim_classify_kernel
+  uint2* ranges;        // MTP0: [B, S_cap/128] smallest and largest score key of each 128-token block
+  uint32_t* hist;       // MTP0: [B, kHistBins] first-digit histogram of the request's keys
+  uint32_t* rowsel;     // MTP0: [B, 4] the request's smallest key, first-digit shift, miss count
+  uint4* gather;        // MTP0: [B, parts, kGatherPart] each chunk's (token, key, pool slot, -) in the threshold's first-digit bin
 };
 
-// MTP3 management runs one workgroup per kChunk-token chunk of a request.
+// Management runs one workgroup per kChunk-token chunk of a request.
 __host__ __device__ inline int64_t mtp_parts(int64_t cap) { return (cap + 4095) / 4096; }
 
-// MTP0 rows longer than kShortRows * 4096 candidates leave the register
-// kernel.  At batches up to kChunkedRows they run chunked (one workgroup per
-// 4096-token chunk, like MTP3); larger batches keep one workgroup per row,
-// which already spreads over as many CUs.
-constexpr int kShortRes = 8;
-constexpr int64_t kChunkedRows = 16;
-__host__ __device__ inline bool chunked_long(int64_t batch, int64_t cap, int queries) {
-  return queries == 1 && batch <= kChunkedRows && cap > kShortRes * 4096;
-}
-
-LimWs carve(void* base, int64_t batch, int64_t cap, int queries) {
-  char* p = static_cast<char*>(base);
-  LimWs w;
-  w.scores = reinterpret_cast<float*>(p);
-  p += align256(sizeof(float) * batch * queries * cap);
-  w.slot_table = reinterpret_cast<uint32_t*>(p);
-  p += align256(sizeof(uint32_t) * batch * kTableStride);
-  w.slot_key = reinterpret_cast<uint32_t*>(p);
-  p += align256(sizeof(uint32_t) * batch * kTableStride);
-  w.miss_list = reinterpret_cast<int32_t*>(p);
-  p += align256(sizeof(int32_t) * batch * kUnionCap);
-  w.select = reinterpret_cast<uint32_t*>(p);
-  p += align256(sizeof(uint32_t) * 4 * batch * queries);
-  w.masks = nullptr;
-  w.part_counts = w.vslot = w.nvict = w.done = nullptr;
+// Workspace layout of one call; with base == nullptr only *bytes is meaningful.
+LimWs lim_layout(void* base, int64_t batch, int64_t cap, int queries, size_t* bytes) {
+  const uintptr_t p0 = reinterpret_cast<uintptr_t>(base);
+  uintptr_t p = p0;
+  auto take = [&](size_t n) {
+    const uintptr_t q = p;
+    p += align256(n);
+    return q;
+  };
+  const size_t B = static_cast<size_t>(batch);
+  LimWs w{};
+  w.scores = reinterpret_cast<float*>(take(sizeof(float) * B * queries * cap));
+  w.slot_table = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * kTableStride));
+  w.slot_key = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * kTableStride));
+  w.select = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4 * B * queries));
+  w.part_counts = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B * mtp_parts(cap) * 8));
+  w.vslot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B * (queries > 1 ? kUnionCap : 2 * kTopK)));
+  w.nvict = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B));
   if (queries > 1) {
-    w.masks = reinterpret_cast<uint8_t*>(p);
-    p += align256(static_cast<size_t>(batch) * cap);
+    w.masks = reinterpret_cast<uint8_t*>(take(B * cap));
+  } else {
+    w.done = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B));
+    w.ranges = reinterpret_cast<uint2*>(take(sizeof(uint2) * B * (cap / kBlock)));
+    w.hist = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * kHistBins));
+    w.rowsel = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4 * B));
+    w.gather = reinterpret_cast<uint4*>(take(sizeof(uint4) * B * mtp_parts(cap) * kGatherPart));
   }
-  if (queries > 1 || chunked_long(batch, cap, queries)) {
-    w.part_counts = reinterpret_cast<int32_t*>(p);
-    p += align256(sizeof(int32_t) * batch * mtp_parts(cap) * 8);
-    w.vslot = reinterpret_cast<int32_t*>(p);
-    p += align256(sizeof(int32_t) * batch * kUnionCap);
-    w.nvict = reinterpret_cast<int32_t*>(p);
-    p += align256(sizeof(int32_t) * batch);
-    w.done = reinterpret_cast<int32_t*>(p);
-  }
+  if (bytes != nullptr) *bytes = p - p0;
   return w;
 }
+
+LimWs carve(void* base, int64_t batch, int64_t cap, int queries) { return lim_layout(base, batch, cap, queries, nullptr); }
 
 // Row guards.  MTP0: ops/fused_li_manage/op_kernel/fused_li_manage_kernel.h:261-290,
 // plus C <= 16383 (the 14-bit slot payload).  MTP3:
@@ -128,14 +127,20 @@ __device__ inline bool lim_mtp_row_valid(int n, int c, int r, int64_t cap, int64
          c <= kMaxCacheTokens && c <= n;
 }
 
+// Order-preserving 32-bit key of a score (one zero: -0 and +0 rank equal).
+__device__ inline uint32_t score_key(float s) { return float_key(s == 0.f ? 0.f : s); }
+
 // ---------------------------------------------------------------------------
 // 1. Scores.
 // RELU = false is the first-decode initialisation score (no ReLU,
 // nanovllm/models/dsa_offload_ops.py:306-311); there `fixed_n` >= 0 gives the
 // candidate count of the single request and the row guards do not apply.
+// For MTP0 management (Q == 1, RELU, side.ranges set) each wave also writes
+// its block's smallest and largest score key, and the workgroups of a request
+// zero the request's state of the chunked management kernels.
 template <typename T, int HEADS, int Q, bool RELU>
 __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs a, float* scores, int mtp,
-                                                                        int fixed_n) {
+                                                                        int fixed_n, LimWs side) {
   __shared__ uint16_t qs[Q * HEADS * kQStride];
   __shared__ float ws[Q * HEADS];
   __shared__ uint4 kstage[kScoreWaves * 32 * kStageStride];
@@ -202,13 +207,29 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-  if (!has_block) return;
+  constexpr bool kRanges = Q == 1 && RELU;
   const int64_t cap = a.source_capacity;
+  if constexpr (kRanges) {
+    if (side.ranges != nullptr) {
+      // The request's first-digit histogram and finished-chunk counter start
+      // at zero; the request's ceil(n / 512) workgroups share the clearing.
+      const int active = static_cast<int>(ceil_div(n, kScoreWaves * kBlock));
+      uint32_t* h = side.hist + static_cast<int64_t>(b) * kHistBins;
+      for (int i = static_cast<int>(blockIdx.x) * kThreads + threadIdx.x; i < kHistBins; i += active * kThreads)
+        h[i] = 0u;
+      if (blockIdx.x == 0 && threadIdx.x == 0) side.done[b] = 0;
+    }
+  }
+  if (!has_block) return;
   float* srow = scores + static_cast<int64_t>(b) * Q * cap;
+  uint2* brange = nullptr;
+  if constexpr (kRanges)
+    if (side.ranges != nullptr) brange = side.ranges + static_cast<int64_t>(b) * (cap / kBlock) + col;
   if (!key_ok) {
     for (int q = 0; q < Q; ++q)
       for (int j = lane; j < kBlock; j += kWave)
         if (t0 + j < n) srow[q * cap + t0 + j] = -FLT_MAX;
+    if (brange != nullptr && lane == 0) *brange = make_uint2(score_key(-FLT_MAX), score_key(-FLT_MAX));
     return;
   }
   // Per 32-token tile, a transpose through the wave's own LDS rows into the
@@ -254,12 +275,29 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
           part[tt] += wv[i] * (RELU ? __int_as_float(max(__float_as_int(acc[i]), 0)) : acc[i]);
       }
     }
+    uint32_t klo = 0xffffffffu, khi = 0u;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       float s = part[tt] + __shfl_xor(part[tt], 32, 64);
       if (s == 0.f) s = 0.f;  // one zero: -0 and +0 rank equal
       const int64_t t = t0 + tt * 32 + col_lane;
-      if (grp == 0 && t < n) srow[q * cap + t] = s;
+      if (grp == 0 && t < n) {
+        srow[q * cap + t] = s;
+        if constexpr (kRanges) {
+          klo = min(klo, score_key(s));
+          khi = max(khi, score_key(s));
+        }
+      }
+    }
+    if constexpr (kRanges) {
+      if (brange != nullptr) {
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+          klo = min(klo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(klo), d, 64)));
+          khi = max(khi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(khi), d, 64)));
+        }
+        if (lane == 0) *brange = make_uint2(klo, khi);
+      }
     }
   }
 }
@@ -278,8 +316,6 @@ struct SelectOut {
   int need_eq;      // elements equal to thresh that belong to the selection
   int cnt_eq;       // elements equal to thresh (INT_MAX when not counted)
 };
-
-__device__ inline uint32_t score_key(float s) { return float_key(s == 0.f ? 0.f : s); }
 
 // Block-wide min / max of 32-bit keys (every thread gets the result).
 __device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
@@ -525,31 +561,6 @@ __device__ inline void load_score_keys(const float* s, int n, int t, uint32_t* k
   }
 }
 
-// Eight consecutive tokens [t0, t0 + 8): raw score bits and pool slots,
-// unconverted (tokens >= n: in = false, raw 0, slot -1).
-__device__ inline void load_raw8(const float* s, const int32_t* pool, int n, int t0, uint32_t* raw, int32_t* slot,
-                                 bool* in) {
-  if (t0 + kItems <= n) {
-    const uint4 a = *reinterpret_cast<const uint4*>(s + t0);
-    const uint4 b = *reinterpret_cast<const uint4*>(s + t0 + 4);
-    const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
-    const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
-    raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
-    raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
-    slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
-    slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) in[e] = true;
-  } else {
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      in[e] = t0 + e < n;
-      raw[e] = in[e] ? __float_as_uint(s[t0 + e]) : 0u;
-      slot[e] = in[e] ? pool[t0 + e] : -1;
-    }
-  }
-}
-
 // Eight consecutive tokens [t0, t0 + 8): score keys and pool slots.
 __device__ inline void load_tokens8(const float* s, const int32_t* pool, int n, int t0, uint32_t* u, int32_t* slot,
                                     bool* in) {
@@ -576,9 +587,10 @@ __device__ inline void load_tokens8(const float* s, const int32_t* pool, int n, 
 
 // Victim slots: the m non-hit slots of [0, c) with the smallest key (free
 // slots first), ascending slot on ties, written in ascending slot order to
-// vslot[0..min(m, #non-hit)).  Returns the number written.
+// vslot[0..min(m, #non-hit)); with vevict, vevict[i] = the unselected token
+// that held slot vslot[i] (-1 for a free slot).  Returns the number written.
 __device__ __forceinline__ int select_victims(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot, uint32_t* hist,
-                              int* scratch, int* bcast, uint32_t* red) {
+                              int* scratch, int* bcast, uint32_t* red, int* vevict = nullptr) {
   const int tid = threadIdx.x;
   if (m <= 0) return 0;
   // inverted keys: the smallest score is the largest inverted key; free slots
@@ -650,7 +662,13 @@ __device__ __forceinline__ int select_victims(int c, int m, const uint32_t* stab
 #pragma unroll
     for (int e = 0; e < kSlotItems; ++e)
       if ((vmask >> e) & 1u) {
-        if (pos < m) vslot[pos] = i0 + e;
+        if (pos < m) {
+          vslot[pos] = i0 + e;
+          if (vevict != nullptr) {
+            const uint32_t ent = stab[i0 + e];
+            vevict[pos] = (ent >> kStateShift) == kStateCand ? static_cast<int>(ent & kTokenMask) : -1;
+          }
+        }
         ++pos;
       }
     run += tot;
@@ -681,15 +699,17 @@ __device__ inline int tie_cutoff_step(unsigned eqm, int t0, int want, int before
 // and tables readable up to ITEMS * kManageThreads entries.
 template <int ITEMS>
 __device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot,
-                                                   uint32_t* hist, int* scratch, int* bcast, uint32_t* red) {
+                                                   uint32_t* hist, int* scratch, int* bcast, uint32_t* red,
+                                                   int* vevict = nullptr) {
   static_assert(ITEMS % 4 == 0, "vector loads of four slots");
   const int tid = threadIdx.x;
   if (m <= 0) return 0;
   const int i0 = tid * ITEMS;
   uint32_t key[ITEMS];
+  uint32_t st[ITEMS];
   unsigned nh = 0u;  // non-hit slots (victim candidates) below c
   {
-    uint32_t st[ITEMS], kv[ITEMS];
+    uint32_t kv[ITEMS];
 #pragma unroll
     for (int j = 0; j < ITEMS / 4; ++j) {
       const uint4 a = *reinterpret_cast<const uint4*>(stab + i0 + 4 * j);
@@ -753,7 +773,11 @@ __device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t*
 #pragma unroll
   for (int e = 0; e < ITEMS; ++e)
     if ((vmask >> e) & 1u) {
-      if (pos < m) vslot[pos] = i0 + e;
+      if (pos < m) {
+        vslot[pos] = i0 + e;
+        if (vevict != nullptr)
+          vevict[pos] = (st[e] >> kStateShift) == kStateCand ? static_cast<int>(st[e] & kTokenMask) : -1;
+      }
       ++pos;
     }
   __syncthreads();
@@ -875,105 +899,110 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
     out[2] = static_cast<uint32_t>(sel.cnt_eq);
     out[3] = static_cast<uint32_t>(cutoff);
   }
-  // The chunked passes (MTP3, long MTP0 rows) start from an all-free slot
-  // table and, for MTP0, a zero count of finished chunks.
+  // The MTP3 passes start from an all-free slot table.
   if (q == 0) {
     uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
     for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
-    if (queries == 1 && tid == 0) w.done[b] = 0;
   }
 }
 
 // ---------------------------------------------------------------------------
-// 2a. MTP0 management.
+// 2a. MTP0 management, three chunked kernels after the scores, one 512-thread
+// workgroup per 4096-token chunk of a request.  (One workgroup per request
+// keeps every pass over the request's tokens on one CU, where each pass is
+// bound by that CU's vector ALUs: 26 us at 32768 candidates.)
+//   lim_hist      the first radix digit (kHistBits wide, relative to the
+//                 request's key range, which the score kernel's per-block
+//                 ranges give) of every key, into the request's histogram
+//                 (LDS, then device atomics); also resets the slot table.
+//   lim_classify  every chunk finds the bin holding the 2048th largest key
+//                 from the histogram and classifies its tokens outside that
+//                 bin (above: selected, below: not): cached tokens go to the
+//                 slot table, misses are counted per chunk, tokens in the bin
+//                 are gathered.  The last chunk of the request to finish (a
+//                 device-scope counter, nobody waits) resolves the threshold
+//                 among the gathered tokens (ties to the lower token),
+//                 classifies them, selects the victims and writes the hit half
+//                 of the output row.
+//   lim_place     every chunk writes its misses after those of the chunks
+//                 before it, paired with the ascending victim slots, and
+//                 updates the pool.
+// The score kernel zeroes each request's histogram, gather count and
+// finished-chunk counter.
+static_assert(kHistBins == 8 * kManageThreads, "lim_classify: eight first-digit bins per thread");
+static_assert(kChunk == 4096, "the gather list holds one chunk's worth of tokens");
 
-// Classify eight consecutive candidates [t0, t0 + 8) of the ordered pass:
-// selection (with ascending-token tie ranks), misses appended in token order,
-// cached tokens recorded in the slot table.  Contains block scans with
-// LDS-only barriers (so the caller's loads of the next tokens stay in
-// flight); the slot table and miss list are read only after the caller's
-// next full barrier.
-__device__ inline void mtp0_classify8(int t0, const uint32_t* u, const int32_t* slot, const bool* in, int c,
-                                      const SelectOut& sel, bool need_rank, int& eq_run, int& miss_run,
-                                      int32_t* misses, uint32_t* stab, uint32_t* skey, int* scratch) {
-  unsigned selmask = 0, eqmask = 0, cachedmask = 0;
-#pragma unroll
-  for (int e = 0; e < kItems; ++e) {
-    if (!in[e]) continue;
-    if (u[e] > sel.thresh) selmask |= 1u << e;
-    if (u[e] == sel.thresh) {
-      if (need_rank) eqmask |= 1u << e;
-      else selmask |= 1u << e;
-    }
-    if (slot[e] >= 0 && slot[e] < c) cachedmask |= 1u << e;
-  }
-  if (need_rank) {
-    int tot;
-    int rk = eq_run + block_exclusive_scan<true>(__popc(eqmask), scratch, &tot);
-#pragma unroll
-    for (int e = 0; e < kItems; ++e)
-      if ((eqmask >> e) & 1u) {
-        if (rk < sel.need_eq) selmask |= 1u << e;
-        ++rk;
-      }
-    eq_run += tot;
-  }
-  const unsigned missmask = selmask & ~cachedmask;
-  int tot;
-  int mp = miss_run + block_exclusive_scan<true>(__popc(missmask), scratch, &tot);
-#pragma unroll
-  for (int e = 0; e < kItems; ++e) {
-    if ((missmask >> e) & 1u) misses[mp++] = t0 + e;
-    if ((cachedmask >> e) & 1u) {
-      if ((selmask >> e) & 1u) {
-        stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateHit << kStateShift);
-      } else {
-        stab[slot[e]] = static_cast<uint32_t>(t0 + e) | (kStateCand << kStateShift);
-        skey[slot[e]] = u[e];
-      }
-    }
-  }
-  miss_run += tot;
+__device__ inline bool mtp0_selected(uint32_t key, int t, uint32_t thr, int cutoff) {
+  return key > thr || (key == thr && t <= cutoff);
 }
 
-__device__ inline void load_pool8(const int32_t* pool, int n, int t0, int32_t* slot) {
+__device__ inline int hist_shift(uint32_t lo, uint32_t hi) {
+  const int bits = hi == lo ? 0 : 32 - __clz(static_cast<int>(hi - lo));
+  return bits > kHistBits ? bits - kHistBits : 0;
+}
+
+// Score keys of tokens [t0, t0 + 8) (tokens >= n: in = false).
+__device__ inline void load_keys8(const float* s, int n, int t0, uint32_t* u, bool* in) {
   if (t0 + kItems <= n) {
-    const int4 pa = *reinterpret_cast<const int4*>(pool + t0);
-    const int4 pb = *reinterpret_cast<const int4*>(pool + t0 + 4);
-    slot[0] = pa.x; slot[1] = pa.y; slot[2] = pa.z; slot[3] = pa.w;
-    slot[4] = pb.x; slot[5] = pb.y; slot[6] = pb.z; slot[7] = pb.w;
+    const float4 x = *reinterpret_cast<const float4*>(s + t0);
+    const float4 y = *reinterpret_cast<const float4*>(s + t0 + 4);
+    u[0] = score_key(x.x); u[1] = score_key(x.y); u[2] = score_key(x.z); u[3] = score_key(x.w);
+    u[4] = score_key(y.x); u[5] = score_key(y.y); u[6] = score_key(y.z); u[7] = score_key(y.w);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) in[e] = true;
   } else {
 #pragma unroll
-    for (int e = 0; e < kItems; ++e) slot[e] = t0 + e < n ? pool[t0 + e] : -1;
+    for (int e = 0; e < kItems; ++e) {
+      in[e] = t0 + e < n;
+      u[e] = in[e] ? score_key(s[t0 + e]) : 0u;
+    }
   }
 }
 
-__device__ __forceinline__ void write_hit_rows(const LimArgs& a, int b, int c, int m, const uint32_t* stab,
-                                               int* scratch);
-
-// Victims, pairing, pool update and the output row of one MTP0 request.
-__device__ __forceinline__ void mtp0_finish(const LimArgs& a, int b, int c, int m, int32_t* pool, uint32_t* stab, uint32_t* skey,
-                            const int32_t* misses, int* vslot, uint32_t* hist, int* scratch, int* bcast,
-                            uint32_t* red) {
+__global__ __launch_bounds__(kManageThreads) void lim_hist_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ uint32_t hist[kHistBins];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
   const int tid = threadIdx.x;
-  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
-  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
-  // Budgets up to 2048 slots: slot states and keys in registers, 4 per thread.
-  const int nv = c <= 4 * kManageThreads ? select_victims_regs<4>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
-                                         : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
-  // Misses first (ascending token), paired with ascending victim slots.
-  for (int i = tid; i < m; i += kManageThreads) {
-    const int t = misses[i];
-    const int d = i < nv ? vslot[i] : -1;
-    out_src[i] = t;
-    out_dst[i] = d;
-    if (d >= 0) {
-      const uint32_t e = stab[d];
-      if ((e >> kStateShift) == kStateCand) pool[e & kTokenMask] = -1;
-      pool[t] = d;
-    }
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows)) {
+    if (part == 0 && tid == 0) a.miss_counts[b] = 0;
+    return;
   }
-  write_hit_rows(a, b, c, m, stab, scratch);
+  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  for (int i = part * kManageThreads + tid; i < c; i += parts * kManageThreads) stab[i] = kStateFree;
+  if (part * kChunk >= n) return;
+  const int64_t cap = a.source_capacity;
+  uint32_t u[kItems];
+  bool in[kItems];
+  load_keys8(w.scores + static_cast<int64_t>(b) * cap, n, part * kChunk + tid * kItems, u, in);
+  const uint2* rg = w.ranges + static_cast<int64_t>(b) * (cap / kBlock);
+  const int nblocks = static_cast<int>(ceil_div(n, kBlock));
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int i = tid; i < nblocks; i += kManageThreads) {
+    const uint2 v = rg[i];
+    lo = min(lo, v.x);
+    hi = max(hi, v.y);
+  }
+  for (int i = tid; i < kHistBins; i += kManageThreads) hist[i] = 0u;
+  block_minmax(lo, hi, red);  // its barriers also order the clearing before the counts
+  const int shift = hist_shift(lo, hi);
+  if (part == 0 && tid == 0) {
+    w.rowsel[4 * b] = lo;
+    w.rowsel[4 * b + 1] = static_cast<uint32_t>(shift);
+  }
+#pragma unroll
+  for (int e = 0; e < kItems; ++e)
+    if (in[e]) atomicAdd(&hist[(u[e] - lo) >> shift], 1u);
+  __syncthreads();
+  uint32_t* gh = w.hist + static_cast<int64_t>(b) * kHistBins;
+  for (int i = tid; i < kHistBins; i += kManageThreads) {
+    const uint32_t v = hist[i];
+    if (v != 0u) atomicAdd(&gh[i], v);
+  }
 }
 
 // The hit half of an MTP0 output row: positions m, m+1, ... get the hits by
@@ -1018,281 +1047,159 @@ __device__ __forceinline__ void write_hit_rows(const LimArgs& a, int b, int c, i
   if (tid == 0) a.miss_counts[b] = m;
 }
 
-// MTP0 management, one workgroup per request.  Each request takes its path
-// from its own candidate count n, whatever the table width:
-// * lim_manage_kernel<RES> takes the rows with n <= RES * kChunk: their
-//   scores live in registers, RES chunks of kChunk tokens (thread t holds
-//   tokens ch*kChunk + 8t .. +8), read from memory once; the radix passes
-//   then touch no memory.  It also answers every invalid row (miss_counts 0).
-// * lim_manage_long_kernel takes the longer rows (launched only when the
-//   table is wider than RES * kChunk tokens): the top-2048 threshold first,
-//   then an ordered pass that streams the scores and pool slots.
-// The two live in separate kernels: in one, the register path's arrays end
-// up in scratch memory (2.5x slower).
-template <int RES>
-__global__ __launch_bounds__(kManageThreads) void lim_manage_kernel(LimArgs a, LimWs w) {
-  static_assert(RES > 0 && RES <= 8, "the packed classification scan holds eight chunks");
-  __shared__ uint32_t hist[kBins];
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint64_t scratch64[2 * (kManageThreads / 64)];
-  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
-  __shared__ int bcast[4];
-  __shared__ int vslot[kTopK];
-  __shared__ int lds_miss[kTopK + kManageThreads];       // + one junk word per thread
-  __shared__ uint32_t lds_stab[kLdsSlots + kManageThreads];
-  __shared__ uint32_t lds_skey[kLdsSlots + kManageThreads];
-  const int b = blockIdx.x;
+// The last chunk of a request in lim_classify_kernel: the threshold among the
+// tokens of the first-digit bin `bin` (the k-th largest of them is the
+// request's 2048th largest key), their classification and the victims.
+// counts[p * 8] holds chunk p's miss count, counts[p * 8 + 1] its in-bin
+// token count (its slice of the gather list holds the first kGatherPart);
+// counts[p * 8 + 2] gets the misses of the chunks before p.
+__device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, int b, int n, int c, int r, int parts,
+                                             int active, uint32_t bin, int k, uint32_t lo, int shift,
+                                             uint32_t* hist, int* scratch, uint32_t* red, int* bcast, int* pcount,
+                                             int* goff, uint32_t* lkey, int* ltok) {
   const int tid = threadIdx.x;
-  const int n = a.num_candidates[b];
-  const int c = a.num_cache[b];
-  const int r = a.pool_entries[b];
-  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows)) {
-    if (tid == 0) a.miss_counts[b] = 0;
-    return;
-  }
-  if (n > RES * kChunk) return;  // lim_manage_long_kernel's row
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + static_cast<int64_t>(b) * cap;
-  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  // Slot tables: LDS for budgets up to kLdsSlots, else the workspace.
-  const bool lds_tables = c <= kLdsSlots;
-  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kTableStride;
-  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kTableStride;
-  int32_t* misses = lds_miss;
-
-  for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  int eq_run = 0, miss_run = 0;
-  {
-    // Scores and pool slots of all the request's tokens, loaded once.  A
-    // slot is kept as 16 bits: 0 <= slot < C (C <= 16383) or 0xffff for
-    // "not cached", which is all the ordered pass distinguishes.  Entries at
-    // t >= n hold whatever the buffers hold there; every later use tests
-    // t < n (masking at load time would let the compiler turn the vector
-    // loads into guarded scalar loads, one wait each).
-    uint32_t u[RES][kItems];
-    uint32_t pk[RES][kItems / 2];
-    auto p16 = [c](int32_t v) -> uint32_t { return (v >= 0 && v < c) ? static_cast<uint32_t>(v) : 0xffffu; };
-    // The row buffers hold cap entries (cap a multiple of 128): a thread's
-    // 8-token group either lies inside or starts at t0 >= cap, whose load is
-    // redirected to the last group and ignored (t0 >= cap >= n).  So every
-    // load is unconditional, and all 32 of a thread's loads are in flight
-    // together.
-    int32_t pr[RES][kItems];
-#pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {  // all loads first (raw bits straight into u / pr) ...
-      const int t0 = ch * kChunk + tid * kItems;
-      const int64_t tl = t0 < cap ? t0 : cap - kItems;
-      const uint4 x = *reinterpret_cast<const uint4*>(s + tl);
-      const uint4 y = *reinterpret_cast<const uint4*>(s + tl + 4);
-      const int4 pa = *reinterpret_cast<const int4*>(pool + tl);
-      const int4 pb = *reinterpret_cast<const int4*>(pool + tl + 4);
-      u[ch][0] = x.x; u[ch][1] = x.y; u[ch][2] = x.z; u[ch][3] = x.w;
-      u[ch][4] = y.x; u[ch][5] = y.y; u[ch][6] = y.z; u[ch][7] = y.w;
-      pr[ch][0] = pa.x; pr[ch][1] = pa.y; pr[ch][2] = pa.z; pr[ch][3] = pa.w;
-      pr[ch][4] = pb.x; pr[ch][5] = pb.y; pr[ch][6] = pb.z; pr[ch][7] = pb.w;
-    }
-#pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {  // ... then the conversions, in place
-#pragma unroll
-      for (int e = 0; e < kItems; ++e) u[ch][e] = score_key(__uint_as_float(u[ch][e]));
-#pragma unroll
-      for (int e = 0; e < kItems / 2; ++e) pk[ch][e] = p16(pr[ch][2 * e]) | (p16(pr[ch][2 * e + 1]) << 16);
-    }
-    uint32_t lo = 0xffffffffu, hi = 0u;
-#pragma unroll
-    for (int ch = 0; ch < RES; ++ch)
-#pragma unroll
-      for (int e = 0; e < kItems; ++e)
-        if (ch * kChunk + tid * kItems + e < n) {
-          lo = min(lo, u[ch][e]);
-          hi = max(hi, u[ch][e]);
-        }
-    block_minmax(lo, hi, red);
-    // Keys relative to the minimum, in place (no per-pass key - kmin copies
-    // for the compiler to keep in registers); the threshold comes back in the
-    // same frame, so the classification compares like with like.
-#pragma unroll
-    for (int ch = 0; ch < RES; ++ch)
-#pragma unroll
-      for (int e = 0; e < kItems; ++e) {
-        u[ch][e] -= lo;
-        // Opaque to the optimiser: otherwise it folds the subtraction into
-        // the later compares and keeps both the absolute and the relative
-        // keys live (spilling).  Emits no instruction.
-        asm volatile("" : "+v"(u[ch][e]));
+  const int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
+  int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
+  // Chunk counts (active <= kManageThreads: one chunk per thread).
+  const int my_in = tid < active ? counts[tid * 8 + 1] : 0;
+  if (tid < active) pcount[tid] = counts[tid * 8];
+  int g;
+  const int off = block_exclusive_scan(min(my_in, kGatherPart), scratch, &g);
+  const bool overflow = __syncthreads_or(my_in > kGatherPart) != 0;
+  if (tid < active) goff[tid] = off;  // ordered before its reads by the barriers below
+  uint32_t thr = 0u;
+  int cutoff = INT_MAX;
+  auto classify = [&](int t, int32_t slot, bool selected, uint32_t key) {
+    if (slot >= 0 && slot < c) {
+      if (selected) {
+        stab[slot] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
+      } else {
+        stab[slot] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
+        skey[slot] = key;
       }
-    const SelectOut sel = radix_select_visit(
-        kTopK, 0u, hi - lo,
-        [&](auto&& fn) {
-#pragma unroll
-          for (int ch = 0; ch < RES; ++ch)
-#pragma unroll
-            for (int e = 0; e < kItems; ++e)
-              if (ch * kChunk + tid * kItems + e < n) fn(u[ch][e]);
-        },
-        hist, scratch, bcast);
-    // One ordered classification pass: token order is (chunk, thread, item),
-    // so the eight chunks' miss counts go through one packed block scan.
-    const bool need_rank = sel.cnt_eq != sel.need_eq;
-    uint32_t selm[RES], eqm[RES], cachm[RES];
-#pragma unroll
-    for (int ch = 0; ch < RES; ++ch) {
-      const int nvalid = n - (ch * kChunk + tid * kItems);  // items e < nvalid are candidates
-      const uint32_t vmask = nvalid >= kItems ? 0xffu : (nvalid <= 0 ? 0u : (1u << nvalid) - 1u);
-      uint32_t sm = 0u, em = 0u, cm = 0u;
-#pragma unroll
-      for (int e = 0; e < kItems; ++e) {
-        sm |= (u[ch][e] > sel.thresh ? 1u : 0u) << e;
-        em |= (u[ch][e] == sel.thresh ? 1u : 0u) << e;
-        cm |= (((pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu) != 0xffffu ? 1u : 0u) << e;
-      }
-      selm[ch] = sm & vmask;
-      eqm[ch] = em & vmask;
-      cachm[ch] = cm & vmask;
+    } else if (selected) {
+      atomicAdd(&pcount[t / kChunk], 1);
     }
-    if (need_rank) {  // ties at the threshold: the lowest tokens first
-      uint64_t cnt[2] = {0, 0}, tot[2];
-#pragma unroll
-      for (int ch = 0; ch < RES; ++ch) cnt[ch >> 2] |= static_cast<uint64_t>(__popc(eqm[ch])) << (16 * (ch & 3));
-      block_exclusive_scan8(cnt, scratch64, tot);
-      int before = 0;
-#pragma unroll
-      for (int ch = 0; ch < RES; ++ch) {
-        int rk = before + lane16x8(cnt, ch);
-#pragma unroll
-        for (int e = 0; e < kItems; ++e)
-          if ((eqm[ch] >> e) & 1u) {
-            if (rk < sel.need_eq) selm[ch] |= 1u << e;
-            ++rk;
-          }
-        before += lane16x8(tot, ch);
+  };
+  if (!overflow && g <= kRankDirect) {
+    // Few tokens in the bin: gather them into LDS and rank them pairwise
+    // (key descending, then token ascending: ties go to the lower token).
+    // Entry f of the list comes from the last chunk p with goff[p] <= f.
+    __syncthreads();  // goff
+    int my_t = 0;
+    uint32_t my_k = 0u;
+    int32_t my_slot = -1;
+    if (tid < g) {
+      int lo_p = 0, hi_p = active - 1;
+      while (lo_p < hi_p) {
+        const int mid = (lo_p + hi_p + 1) >> 1;
+        if (goff[mid] <= tid) lo_p = mid;
+        else hi_p = mid - 1;
       }
-    } else {
-#pragma unroll
-      for (int ch = 0; ch < RES; ++ch) selm[ch] |= eqm[ch];
+      const uint4 e = w.gather[(static_cast<int64_t>(b) * parts + lo_p) * kGatherPart + (tid - goff[lo_p])];
+      my_t = static_cast<int>(e.x);
+      my_k = e.y;
+      my_slot = static_cast<int32_t>(e.z);
+      ltok[tid] = my_t;
+      lkey[tid] = my_k;
     }
-    uint64_t cnt[2] = {0, 0}, tot[2];
-#pragma unroll
-    for (int ch = 0; ch < RES; ++ch)
-      cnt[ch >> 2] |= static_cast<uint64_t>(__popc(selm[ch] & ~cachm[ch])) << (16 * (ch & 3));
-    block_exclusive_scan8(cnt, scratch64, tot);
-    // Every item stores unconditionally: entries it does not own go to this
-    // thread's junk word past the slot table (no divergent branch per item;
-    // about 1 item in 15 is cached or missed).  Two instantiations keep the
-    // LDS tables on ds_write (a pointer that may be either is a flat store).
-    auto write_items = [&](uint32_t* tab, uint32_t* key, uint32_t junk) {
-      int tb = tid;
-      asm volatile("" : "+v"(tb));  // token ids are formed here, not hoisted into the radix passes
-#pragma unroll
-      for (int ch = 0; ch < RES; ++ch) {
-        int pos = miss_run + lane16x8(cnt, ch);
-        const int t0 = ch * kChunk + tb * kItems;
-        const uint32_t missm = selm[ch] & ~cachm[ch];
-#pragma unroll
-        for (int e = 0; e < kItems; ++e) {
-          const bool miss = (missm >> e) & 1u;
-          lds_miss[miss ? pos : kTopK + tid] = t0 + e;
-          pos += miss ? 1 : 0;
-          const bool cached = (cachm[ch] >> e) & 1u;
-          const bool hit = (selm[ch] >> e) & 1u;
-          const uint32_t slot = (pk[ch][e >> 1] >> (16 * (e & 1))) & 0xffffu;
-          tab[cached ? slot : junk] = static_cast<uint32_t>(t0 + e) | ((hit ? kStateHit : kStateCand) << kStateShift);
-          key[cached && !hit ? slot : junk] = u[ch][e] + lo;  // absolute key (free slots rank below every score)
-        }
-        miss_run += lane16x8(tot, ch);
+    __syncthreads();
+    if (tid < g) {
+      int rank = 0;
+      for (int j = 0; j < g; ++j) {
+        const uint32_t kj = lkey[j];
+        rank += (kj > my_k || (kj == my_k && ltok[j] < my_t)) ? 1 : 0;
       }
+      if (rank == k - 1) {  // the last selected token: the threshold and the tie cutoff
+        bcast[0] = static_cast<int>(my_k);
+        bcast[1] = my_t;
+      }
+      classify(my_t, my_slot, rank < k, my_k);
+    }
+    __syncthreads();
+    thr = static_cast<uint32_t>(bcast[0]);
+    cutoff = bcast[1];
+  } else {
+    // More tokens in the bin than the lists hold (heavy ties, or a key range
+    // stretched by unmapped index blocks): stream the request's scores.
+    for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+    __syncthreads();
+    const uint32_t klo = lo + (bin << shift);  // keys in the bin lie in [klo, khi]
+    const uint64_t top = static_cast<uint64_t>(klo) + ((uint64_t{1} << shift) - 1u);
+    const uint32_t khi = top > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(top);
+    const int ngroups = static_cast<int>(ceil_div(n, 4));
+    auto load_bin = [&](int gi, uint32_t* key, bool* inc) {
+      load_score_keys(s, n, 4 * gi, key, inc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) inc[e] = inc[e] && ((key[e] - lo) >> shift) == bin;
     };
-    if (lds_tables)
-      write_items(lds_stab, lds_skey, kLdsSlots + tid);
-    else
-      write_items(stab, skey, kSlotStride + tid);
-  }
-  __syncthreads();
-  mtp0_finish(a, b, c, miss_run, pool, stab, skey, misses, vslot, hist, scratch, bcast, red);
-}
-
-// The rows longer than SHORT * kChunk candidates (see lim_manage_kernel):
-// threshold with the keys in registers (TRES chunks, TRES * kChunk >= every
-// such row) or streamed (TRES == 0), then the streamed ordered pass.
-template <int SHORT, int TRES>
-__global__ __launch_bounds__(kManageThreads) void lim_manage_long_kernel(LimArgs a, LimWs w) {
-  __shared__ uint32_t hist[kBins];
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
-  __shared__ int bcast[4];
-  __shared__ int vslot[kTopK];
-  __shared__ int lds_miss[kTopK];
-  __shared__ uint32_t lds_stab[kLdsSlots];
-  __shared__ uint32_t lds_skey[kLdsSlots];
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int n = a.num_candidates[b];
-  const int c = a.num_cache[b];
-  const int r = a.pool_entries[b];
-  // Invalid rows are answered by lim_manage_kernel; short rows are its own.
-  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || n <= SHORT * kChunk) return;
-  const int64_t cap = a.source_capacity;
-  const float* s = w.scores + static_cast<int64_t>(b) * cap;
-  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  const bool lds_tables = c <= kLdsSlots;
-  uint32_t* stab = lds_tables ? lds_stab : w.slot_table + static_cast<int64_t>(b) * kTableStride;
-  uint32_t* skey = lds_tables ? lds_skey : w.slot_key + static_cast<int64_t>(b) * kTableStride;
-  int32_t* misses = lds_miss;
-  for (int i = tid; i < c; i += kManageThreads) stab[i] = kStateFree;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  int eq_run = 0, miss_run = 0;
-  {
-    const SelectOut sel = row_threshold<TRES>(s, n, cap, hist, scratch, bcast, red);
-    const bool need_rank = sel.cnt_eq != sel.need_eq;
-    // Software-pipelined: the next chunk's raw scores and slots are loaded
-    // before this chunk is classified, and converted to keys only when used.
-    uint32_t raw[kItems];
-    int32_t slot[kItems];
-    bool in[kItems];
-    load_raw8(s, pool, n, tid * kItems, raw, slot, in);
-    for (int base = 0; base < n; base += kChunk) {
-      uint32_t u[kItems];
+    const SelectOut sel = radix_select(ngroups, k, klo, khi, load_bin, hist, scratch, bcast);
+    thr = sel.thresh;
+    if (sel.need_eq != sel.cnt_eq) {  // ties at the threshold: one ordered pass finds the last selected
+      int before = 0;
+      for (int g0 = 0; g0 < ngroups; g0 += kManageThreads) {
+        const int gi = g0 + tid;
+        unsigned eqm = 0u;
+        if (gi < ngroups) {
+          uint32_t key[4];
+          bool inc[4];
+          load_bin(gi, key, inc);
 #pragma unroll
-      for (int e = 0; e < kItems; ++e) u[e] = in[e] ? score_key(__uint_as_float(raw[e])) : 0u;
-      int32_t cur_slot[kItems];
-      bool cur_in[kItems];
-#pragma unroll
-      for (int e = 0; e < kItems; ++e) {
-        cur_slot[e] = slot[e];
-        cur_in[e] = in[e];
+          for (int e = 0; e < 4; ++e)
+            if (inc[e] && key[e] == thr) eqm |= 1u << e;
+        }
+        before = tie_cutoff_step(eqm, 4 * gi, sel.need_eq - 1, before, scratch, bcast);
       }
-      if (base + kChunk < n) load_raw8(s, pool, n, base + kChunk + tid * kItems, raw, slot, in);  // uniform
-      mtp0_classify8(base + tid * kItems, u, cur_slot, cur_in, c, sel, need_rank, eq_run, miss_run, misses, stab,
-                     skey, scratch);
+      __syncthreads();
+      cutoff = bcast[3];
+    }
+    for (int gi = tid; gi < ngroups; gi += kManageThreads) {
+      uint32_t key[4];
+      bool inc[4];
+      load_bin(gi, key, inc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (inc[e]) classify(4 * gi + e, pool[4 * gi + e], mtp0_selected(key[e], 4 * gi + e, thr, cutoff), key[e]);
     }
   }
+  if (tid == 0) {
+    uint32_t* out = w.select + static_cast<int64_t>(b) * 4;
+    out[0] = thr;
+    out[3] = static_cast<uint32_t>(cutoff);
+  }
+  __syncthreads();  // the slot table and the chunk counts are complete
+  const int mine = tid < active ? pcount[tid] : 0;
+  int total;
+  const int before = block_exclusive_scan(mine, scratch, &total);
+  if (tid < active) counts[tid * 8 + 2] = before;
+  const int m = min(total, kTopK);  // misses are selected tokens
+  if (tid == 0) w.rowsel[4 * b + 2] = static_cast<uint32_t>(m);
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   __syncthreads();
-  mtp0_finish(a, b, c, miss_run, pool, stab, skey, misses, vslot, hist, scratch, bcast, red);
+  // Budgets up to 2048 slots hold the slot states in registers (4 per thread);
+  // larger ones stream them (a 16-per-thread variant here costs the kernel
+  // its second workgroup per CU: 144 instead of 116 VGPRs).
+  int32_t* vslot = w.vslot + static_cast<int64_t>(b) * 2 * kTopK;
+  const int nv = c <= 4 * kManageThreads
+                     ? select_victims_regs<4>(c, m, stab, skey, vslot, hist, scratch, bcast, red, vslot + kTopK)
+                     : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red, vslot + kTopK);
+  if (tid == 0) w.nvict[b] = nv;
 }
 
-// Long MTP0 rows (more than kShortRes * kChunk candidates) at batches up to
-// kChunkedRows, one workgroup per 4096-token chunk of a request, after
-// lim_threshold_kernel (threshold key and tie cutoff per row, slot table
-// reset, finished-chunk count zeroed):
-//   pass A   each chunk classifies its tokens (selected: key above the
-//            threshold, or equal with token <= cutoff), records cached tokens
-//            in the slot table and counts its misses; the last chunk of the
-//            request to finish (a device-scope counter, no waiting) selects
-//            the victims and writes the hit half of the output row;
-//   pass B   each chunk writes its misses after those of the chunks before
-//            it, paired with the ascending victim slots, and updates the pool.
-// Pass B reads pool entries only of selected tokens: evictions rewrite
-// entries of unselected tokens only, and a miss's entry only its own chunk.
-__device__ inline bool mtp0_selected(uint32_t key, int t, uint32_t thr, int cutoff) {
-  return key > thr || (key == thr && t <= cutoff);
-}
-
-__global__ __launch_bounds__(kManageThreads) void lim_long_pass_a_kernel(LimArgs a, LimWs w, int parts) {
+__global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a, LimWs w, int parts) {
   __shared__ uint32_t hist[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
+  __shared__ int pcount[kManageThreads];
+  __shared__ int goff[kManageThreads];
+  __shared__ uint32_t lkey[kRankDirect];
+  __shared__ int ltok[kRankDirect];
   __shared__ int last;
   const int b = blockIdx.x / parts;
   const int part = blockIdx.x - b * parts;
@@ -1300,42 +1207,87 @@ __global__ __launch_bounds__(kManageThreads) void lim_long_pass_a_kernel(LimArgs
   const int n = a.num_candidates[b];
   const int c = a.num_cache[b];
   const int r = a.pool_entries[b];
-  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || n <= kShortRes * kChunk) return;
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || part * kChunk >= n) return;
+  const int active = static_cast<int>(ceil_div(n, kChunk));  // chunks that arrive below
   const int64_t cap = a.source_capacity;
-  int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
-  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
-  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
-  int my_miss = 0;
-  if (part * kChunk < n) {
-    const uint32_t* sel = w.select + static_cast<int64_t>(b) * 4;
-    const uint32_t thr = sel[0];
-    const int cutoff = static_cast<int>(sel[3]);
-    const float* s = w.scores + static_cast<int64_t>(b) * cap;
-    const int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-    const int t0 = part * kChunk + tid * kItems;
-    uint32_t u[kItems];
-    int32_t slot[kItems];
-    bool in[kItems];
-    load_tokens8(s, pool, n, t0, u, slot, in);
+  const uint32_t lo = w.rowsel[4 * b];
+  const int shift = static_cast<int>(w.rowsel[4 * b + 1]);
+  // This chunk's tokens: the loads are in flight during the bin search.
+  const int t0 = part * kChunk + tid * kItems;
+  uint32_t u[kItems];
+  int32_t slot[kItems];
+  bool in[kItems];
+  load_tokens8(w.scores + static_cast<int64_t>(b) * cap, a.pool + static_cast<int64_t>(r) * cap, n, t0, u, slot, in);
+  // The first-digit bin holding the 2048th largest key: thread tid owns bins
+  // [8 tb, 8 tb + 8), tb = 511 - tid, so ascending threads scan descending bins.
+  int bin = 0, above = 0;
+  {
+    const int tb = kManageThreads - 1 - tid;
+    const uint32_t* gh = w.hist + static_cast<int64_t>(b) * kHistBins + 8 * tb;
+    const uint4 h0 = *reinterpret_cast<const uint4*>(gh);
+    const uint4 h1 = *reinterpret_cast<const uint4*>(gh + 4);
+    const int cnt[8] = {static_cast<int>(h0.x), static_cast<int>(h0.y), static_cast<int>(h0.z), static_cast<int>(h0.w),
+                        static_cast<int>(h1.x), static_cast<int>(h1.y), static_cast<int>(h1.z), static_cast<int>(h1.w)};
+    int sum = 0;
 #pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      if (!in[e]) continue;
-      const int t = t0 + e;
-      const bool selected = mtp0_selected(u[e], t, thr, cutoff);
-      if (slot[e] >= 0 && slot[e] < c) {
-        if (selected) {
-          stab[slot[e]] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
-        } else {
-          stab[slot[e]] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
-          skey[slot[e]] = u[e];
+    for (int j = 0; j < 8; ++j) sum += cnt[j];
+    if (tid == 0) bcast[0] = bcast[1] = 0;  // ordered before the writes below by the scan's barriers
+    int total;
+    int acc = block_exclusive_scan(sum, scratch, &total);
+    if (acc < kTopK && kTopK <= acc + sum) {
+#pragma unroll
+      for (int j = 7; j >= 0; --j) {
+        if (acc < kTopK && kTopK <= acc + cnt[j]) {
+          bcast[0] = 8 * tb + j;
+          bcast[1] = acc;
         }
-      } else if (selected) {
-        ++my_miss;
+        acc += cnt[j];
       }
     }
+    __syncthreads();
+    bin = __builtin_amdgcn_readfirstlane(bcast[0]);
+    above = __builtin_amdgcn_readfirstlane(bcast[1]);
   }
-  const int chunk_misses = block_sum(my_miss, scratch);
-  if (tid == 0) counts[part * 8] = chunk_misses;
+  uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
+  unsigned missm = 0u, inbin = 0u;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    if (!in[e]) continue;
+    const uint32_t d = (u[e] - lo) >> shift;
+    if (d == static_cast<uint32_t>(bin)) {
+      inbin |= 1u << e;
+      continue;
+    }
+    const bool selected = d > static_cast<uint32_t>(bin);
+    const int t = t0 + e;
+    if (slot[e] >= 0 && slot[e] < c) {
+      if (selected) {
+        stab[slot[e]] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
+      } else {
+        stab[slot[e]] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
+        skey[slot[e]] = u[e];
+      }
+    } else if (selected) {
+      missm |= 1u << e;
+    }
+  }
+  // One scan for both counts (each below 2^16): misses high, in-bin tokens low.
+  uint64_t tot;
+  const uint64_t pos = block_exclusive_scan4(static_cast<uint64_t>(__popc(missm)) << 16 | __popc(inbin), scratch64, &tot);
+  int idx = static_cast<int>(pos & 0xffffu);
+  uint4* gl = w.gather + (static_cast<int64_t>(b) * parts + part) * kGatherPart;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e)
+    if ((inbin >> e) & 1u) {
+      if (idx < kGatherPart) gl[idx] = make_uint4(static_cast<uint32_t>(t0 + e), u[e], static_cast<uint32_t>(slot[e]), 0u);
+      ++idx;
+    }
+  int32_t* counts = w.part_counts + (static_cast<int64_t>(b) * parts + part) * 8;
+  if (tid == 0) {
+    counts[0] = static_cast<int>((tot >> 16) & 0xffffu);
+    counts[1] = static_cast<int>(tot & 0xffffu);
+  }
   // The barrier waits for every wave's stores; one release fence then makes
   // them visible device-wide before the arrival count, and the last chunk of
   // the request to arrive acquires the others' (one agent-scope fence each
@@ -1344,72 +1296,57 @@ __global__ __launch_bounds__(kManageThreads) void lim_long_pass_a_kernel(LimArgs
   __syncthreads();
   if (tid == 0) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    last = atomicAdd(&w.done[b], 1) == parts - 1 ? 1 : 0;
+    last = atomicAdd(&w.done[b], 1) == active - 1 ? 1 : 0;
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!last) return;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  int local = 0;
-  for (int p = tid; p < parts; p += kManageThreads) local += counts[p * 8];
-  const int m = block_sum(local, scratch);  // also orders the hist clearing before the selects
-  int32_t* vslot = w.vslot + static_cast<int64_t>(b) * kUnionCap;
-  const int nv = c <= 4 * kManageThreads    ? select_victims_regs<4>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
-                 : c <= 16 * kManageThreads ? select_victims_regs<16>(c, m, stab, skey, vslot, hist, scratch, bcast, red)
-                                            : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red);
-  if (tid == 0) w.nvict[b] = nv;
-  write_hit_rows(a, b, c, m, stab, scratch);
+  mtp0_resolve(a, w, b, n, c, r, parts, active, static_cast<uint32_t>(bin), kTopK - above, lo, shift, hist, scratch,
+               red, bcast, pcount, goff, lkey, ltok);
 }
 
-__global__ __launch_bounds__(kManageThreads) void lim_long_pass_b_kernel(LimArgs a, LimWs w, int parts) {
+// Every chunk writes its misses after those of the chunks before it, paired
+// with the ascending victim slots, and updates the pool; one more workgroup
+// per request (part == parts) writes the hit half of the output row.  Pool
+// entries are read only of selected tokens: evictions rewrite entries of
+// unselected tokens only, and a miss's entry only its own chunk.
+__global__ __launch_bounds__(kManageThreads) void lim_place_kernel(LimArgs a, LimWs w, int parts) {
   __shared__ int scratch[kManageThreads / 64 + 1];
-  const int b = blockIdx.x / parts;
-  const int part = blockIdx.x - b * parts;
+  const int b = blockIdx.x / (parts + 1);
+  const int part = blockIdx.x - b * (parts + 1);
   const int tid = threadIdx.x;
   const int n = a.num_candidates[b];
   const int c = a.num_cache[b];
   const int r = a.pool_entries[b];
-  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || n <= kShortRes * kChunk) return;
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows)) return;
+  const uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
+  if (part == parts) {
+    write_hit_rows(a, b, c, static_cast<int>(w.rowsel[4 * b + 2]), stab, scratch);
+    return;
+  }
   if (part * kChunk >= n) return;
   const int64_t cap = a.source_capacity;
-  const int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
-  int local = 0;
-  for (int p = tid; p < part; p += kManageThreads) local += counts[p * 8];
-  const int before = block_sum(local, scratch);  // misses of the chunks before this one
+  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  // Every load that does not depend on another is issued first.
+  const int before = w.part_counts[(static_cast<int64_t>(b) * parts + part) * 8 + 2];  // misses of earlier chunks
   const uint32_t* sel = w.select + static_cast<int64_t>(b) * 4;
   const uint32_t thr = sel[0];
   const int cutoff = static_cast<int>(sel[3]);
   const int nv = w.nvict[b];
-  const int32_t* vslot = w.vslot + static_cast<int64_t>(b) * kUnionCap;
-  const uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
-  const float* s = w.scores + static_cast<int64_t>(b) * cap;
-  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
-  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
   const int t0 = part * kChunk + tid * kItems;
   uint32_t u[kItems];
+  int32_t slot[kItems];
   bool in[kItems];
-  if (t0 + kItems <= n) {
-    const float4 x = *reinterpret_cast<const float4*>(s + t0);
-    const float4 y = *reinterpret_cast<const float4*>(s + t0 + 4);
-    u[0] = score_key(x.x); u[1] = score_key(x.y); u[2] = score_key(x.z); u[3] = score_key(x.w);
-    u[4] = score_key(y.x); u[5] = score_key(y.y); u[6] = score_key(y.z); u[7] = score_key(y.w);
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) in[e] = true;
-  } else {
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      in[e] = t0 + e < n;
-      u[e] = in[e] ? score_key(s[t0 + e]) : 0u;
-    }
-  }
+  load_tokens8(w.scores + static_cast<int64_t>(b) * cap, pool, n, t0, u, slot, in);
+  const int32_t* vslot = w.vslot + static_cast<int64_t>(b) * 2 * kTopK;
+  const int32_t* vevict = vslot + kTopK;
+  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
+  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
+  // Only selected tokens' slots are used: their entries are this chunk's alone.
   unsigned missm = 0u;
 #pragma unroll
-  for (int e = 0; e < kItems; ++e) {
-    if (!in[e] || !mtp0_selected(u[e], t0 + e, thr, cutoff)) continue;
-    const int32_t slot = pool[t0 + e];  // a selected token: no other chunk writes its entry
-    if (!(slot >= 0 && slot < c)) missm |= 1u << e;
-  }
+  for (int e = 0; e < kItems; ++e)
+    if (in[e] && mtp0_selected(u[e], t0 + e, thr, cutoff) && !(slot[e] >= 0 && slot[e] < c)) missm |= 1u << e;
   int tot;
   int pos = before + block_exclusive_scan(__popc(missm), scratch, &tot);
 #pragma unroll
@@ -1417,13 +1354,13 @@ __global__ __launch_bounds__(kManageThreads) void lim_long_pass_b_kernel(LimArgs
     if (!((missm >> e) & 1u)) continue;
     const int t = t0 + e;
     const int d = pos < nv ? vslot[pos] : -1;
+    const int evicted = pos < nv ? vevict[pos] : -1;  // an unselected token, or -1 for a free slot
     if (pos < kTopK) {
       out_src[pos] = t;
       out_dst[pos] = d;
     }
     if (d >= 0) {
-      const uint32_t ent = stab[d];
-      if ((ent >> kStateShift) == kStateCand) pool[ent & kTokenMask] = -1;  // an unselected token
+      if (evicted >= 0) pool[evicted] = -1;
       pool[t] = d;
     }
     ++pos;
@@ -1840,10 +1777,10 @@ hipError_t launch_lidu_scores(const LiduInitArgs& a, const InitWs& w, hipStream_
   const dim3 grid(static_cast<uint32_t>(ceil_div(ceil_div(a.n, kBlock), kScoreWaves)), 1);
   if (a.heads == 32) {
     launch_kernel(kKernLimScore, lim_score_kernel<T, 32, 1, false>, grid, dim3(kScoreWaves * kWave), stream, la,
-                  w.scores, 0, static_cast<int>(a.n));
+                  w.scores, 0, static_cast<int>(a.n), LimWs{});
   } else {
     launch_kernel(kKernLimScore, lim_score_kernel<T, 64, 1, false>, grid, dim3(kScoreWaves * kWave), stream, la,
-                  w.scores, 0, static_cast<int>(a.n));
+                  w.scores, 0, static_cast<int>(a.n), LimWs{});
   }
   return hipGetLastError();
 }
@@ -1853,42 +1790,35 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   const LimWs w = carve(a.workspace, a.batch, a.source_capacity, Q);
   const dim3 grid(static_cast<uint32_t>(ceil_div(a.cols, kScoreWaves)), static_cast<uint32_t>(a.batch));
   const int mtp = Q > 1 ? 1 : 0;
+  const int parts = static_cast<int>(mtp_parts(a.source_capacity));
+  // The chunk counts are scanned one part per thread (MTP3 pass B, MTP0's last chunk).
+  if (parts > kManageThreads) return hipErrorInvalidValue;
+  // MTP0: the score kernel also writes the per-block key ranges and zeroes the chunked passes' state.
+  const LimWs side = Q == 1 ? w : LimWs{};
   if (a.heads == 32) {
     launch_kernel(kKernLimScore, lim_score_kernel<T, 32, Q, true>, grid, dim3(kScoreWaves * kWave), stream, a,
-                  w.scores, mtp, -1);
+                  w.scores, mtp, -1, side);
   } else {
     launch_kernel(kKernLimScore, lim_score_kernel<T, 64, Q, true>, grid, dim3(kScoreWaves * kWave), stream, a,
-                  w.scores, mtp, -1);
+                  w.scores, mtp, -1, side);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 mgrid(static_cast<uint32_t>(a.batch)), mblock(kManageThreads);
   const dim3 tgrid(static_cast<uint32_t>(a.batch * Q));
-  const int parts = static_cast<int>(mtp_parts(a.source_capacity));
-  if (parts > kManageThreads) return hipErrorInvalidValue;  // MTP3 pass B scans one part per thread
   const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
-  auto launch_threshold = [&](int min_n) {
-    if (a.source_capacity <= 16 * kChunk)
-      launch_kernel(kKernLimThreshold, lim_threshold_kernel<16>, tgrid, mblock, stream, a, w, Q, min_n);
-    else
-      launch_kernel(kKernLimThreshold, lim_threshold_kernel<0>, tgrid, mblock, stream, a, w, Q, min_n);
-  };
-  if (Q == 1) {  // each request takes its path from its own candidate count
-    launch_kernel(kKernLimManage, lim_manage_kernel<kShortRes>, mgrid, mblock, stream, a, w);
-    if (a.source_capacity <= kShortRes * kChunk) return hipGetLastError();  // no row can be longer
-    if (chunked_long(a.batch, a.source_capacity, Q)) {
-      launch_threshold(kShortRes * kChunk + 1);
-      launch_kernel(kKernLimLongPassA, lim_long_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
-      launch_kernel(kKernLimLongPassB, lim_long_pass_b_kernel, pgrid, mblock, stream, a, w, parts);
-    } else if (a.source_capacity <= 16 * kChunk) {
-      launch_kernel(kKernLimManageLong, lim_manage_long_kernel<kShortRes, 16>, mgrid, mblock, stream, a, w);
-    } else {
-      launch_kernel(kKernLimManageLong, lim_manage_long_kernel<kShortRes, 0>, mgrid, mblock, stream, a, w);
-    }
+  if (Q == 1) {
+    launch_kernel(kKernLimHist, lim_hist_kernel, pgrid, mblock, stream, a, w, parts);
+    launch_kernel(kKernLimClassify, lim_classify_kernel, pgrid, mblock, stream, a, w, parts);
+    launch_kernel(kKernLimPlace, lim_place_kernel, dim3(static_cast<uint32_t>(a.batch * (parts + 1))), mblock, stream,
+                  a, w, parts);
     return hipGetLastError();
   }
   // MTP3: thresholds first, one workgroup per (request, query) score row.
-  launch_threshold(0);
+  if (a.source_capacity <= 16 * kChunk)
+    launch_kernel(kKernLimThreshold, lim_threshold_kernel<16>, tgrid, mblock, stream, a, w, Q, 0);
+  else
+    launch_kernel(kKernLimThreshold, lim_threshold_kernel<0>, tgrid, mblock, stream, a, w, Q, 0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_kernel(kKernLimMtpPassA, lim_mtp_pass_a_kernel, pgrid, mblock, stream, a, w, parts);
@@ -1900,17 +1830,9 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
 }  // namespace
 
 size_t lim_workspace_bytes(int64_t batch, int64_t source_capacity, int queries) {
-  size_t total = align256(sizeof(float) * batch * queries * source_capacity);
-  total += 2 * align256(sizeof(uint32_t) * batch * kTableStride);
-  total += align256(sizeof(int32_t) * batch * kUnionCap);
-  total += align256(sizeof(uint32_t) * 4 * batch * queries);
-  if (queries > 1) total += align256(static_cast<size_t>(batch) * source_capacity);
-  if (queries > 1 || chunked_long(batch, source_capacity, queries)) {
-    total += align256(sizeof(int32_t) * batch * mtp_parts(source_capacity) * 8);
-    total += align256(sizeof(int32_t) * batch * kUnionCap);
-    total += 2 * align256(sizeof(int32_t) * batch);
-  }
-  return total;
+  size_t bytes = 0;
+  (void)lim_layout(nullptr, batch, source_capacity, queries, &bytes);
+  return bytes;
 }
 
 size_t lidu_init_workspace_bytes(int64_t source_capacity) {

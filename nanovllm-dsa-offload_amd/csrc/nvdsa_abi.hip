@@ -178,13 +178,13 @@ int nvdsa_profile_end(float* durations_ms, int32_t* kernel_ids, int32_t capacity
 }
 
 const char* nvdsa_kernel_name(int32_t kernel_id) {
-  static const char* names[] = {"scatter_copy_kernel", "lim_score_kernel",   "lim_manage_kernel",
+  static const char* names[] = {"scatter_copy_kernel", "lim_score_kernel",   "lim_hist_kernel",
                                 "lim_mtp_pass_a_kernel", "sfa_split_kernel", "sfa_split_kernel_fused",
                                 "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel",
                                 "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
                                 "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied", "indexer_project_kernel",
-                                "indexer_rope_kernel", "persist_blocks_kernel", "lim_manage_long_kernel",
-                                "lim_long_pass_a_kernel", "lim_long_pass_b_kernel"};
+                                "indexer_rope_kernel", "persist_blocks_kernel", "lim_classify_kernel",
+                                "lim_place_kernel"};
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }

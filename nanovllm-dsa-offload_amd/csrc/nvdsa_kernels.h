@@ -15,7 +15,7 @@ enum class Elem { kBf16, kF16 };
 enum KernelId : int {
   kKernScatter = 0,
   kKernLimScore = 1,
-  kKernLimManage = 2,
+  kKernLimHist = 2,
   kKernLimMtpPassA = 3,
   kKernSfaSplit = 4,
   kKernSfaSplitFused = 5,
@@ -30,10 +30,9 @@ enum KernelId : int {
   kKernIdxProject = 14,
   kKernIdxRope = 15,
   kKernPersist = 16,
-  kKernLimManageLong = 17,
-  kKernLimLongPassA = 18,
-  kKernLimLongPassB = 19,
-  kKernCount = 20
+  kKernLimClassify = 17,
+  kKernLimPlace = 18,
+  kKernCount = 19
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.

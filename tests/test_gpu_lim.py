@@ -204,8 +204,10 @@ def _tie_case(mtp: bool, positives, seed=11, n_tokens=12288):
     return case
 
 
-# 40960-token rows take the chunked path for long rows (batch <= 16).
-TIE_CASES = [(False, [700], 12288), (False, [700], 40960), (True, [500, 900, 1300, 1900], 12288)]
+# MTP0: at 4096 tokens the 3396 tied zeros fit the threshold bin's gather
+# list; at 12288 and 40960 they overflow it and the last chunk streams the row.
+TIE_CASES = [(False, [700], 4096), (False, [700], 12288), (False, [700], 40960),
+             (True, [500, 900, 1300, 1900], 12288)]
 
 
 @pytest.mark.parametrize("mtp,positives,n_tokens", TIE_CASES)
@@ -256,11 +258,11 @@ def test_lim_unmapped_index_blocks_score_lowest(mtp, positives, n_tokens):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_lim_long_rows_small_batch_bit_exact(dtype):
-    """Rows past 32768 candidates at a small batch run chunked (a workgroup
-    per 4096 tokens, the last chunk to finish picking the victims): long rows
-    with C = 2048, 6144 and 12288 (the three victim selects) beside a short
-    row with its slot tables in the workspace; every output and the pool
-    bit-exact, and the repeat call has no misses."""
+    """Rows of 20480 to 65536 candidates (5 to 16 chunks of 4096 tokens, the
+    last chunk of a request to finish resolving the threshold and picking the
+    victims) with C = 2048, 6144 and 12288 (the three victim selects: four
+    and sixteen slots per thread in registers, streamed); every output and
+    the pool bit-exact, and the repeat call has no misses."""
     from nanovllm_amd.workloads import make_chain_case
 
     case = make_chain_case(4, [40960, 65536, 20480, 49152], [2048, 6144, 12288, 12288], [3, 64, 127, 9], seed=23,
