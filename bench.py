@@ -87,7 +87,7 @@ def parse_args():
 
 # ---- hardware-counter helpers ------------------------------------------------
 # The MTP0 management kernels, in launch order (one workgroup per 4096-token chunk).
-MANAGE_KERNELS = ("lim_hist_kernel", "lim_classify_kernel", "lim_place_kernel")
+MANAGE_KERNELS = ("lim_hist_kernel", "lim_classify_kernel")
 PMC_KERNELS = ("lim_score_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
                "lim_threshold_kernel") + MANAGE_KERNELS + ("sfa_split_kernel",
                "sfa_combine_kernel", "scatter_copy_kernel", "indexer_project_kernel")

@@ -11,7 +11,7 @@
 //   2. management, chunked: one 512-thread workgroup per 4096-token chunk of
 //      a request — the top-2048 threshold, the ordered pass over the
 //      candidates against the request's pool row, victim selection, pairing
-//      and pool update (MTP0: lim_hist / lim_classify / lim_place; MTP3:
+//      and pool update (MTP0: lim_hist / lim_classify; MTP3:
 //      lim_threshold / lim_mtp_pass_a / lim_mtp_victims / lim_mtp_pass_b).
 //
 // Canonical semantics (the reference leaves victim choice and in-row order
@@ -52,6 +52,7 @@ constexpr int kHistBits = 12;                     // MTP0: first digit of the ch
 constexpr int kHistBins = 1 << kHistBits;
 constexpr int kGatherPart = 128;                  // MTP0: in-bin tokens a chunk can hand over
 constexpr int kRankDirect = 512;                  // MTP0: in-bin tokens ranked pairwise by the last chunk
+constexpr int kMissPart = 256;                    // MTP0: definite misses a chunk can hand over
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr int kTableStride = kSlotStride + kManageThreads;  // workspace slot tables: + one junk word per thread
 constexpr uint32_t kStateShift = 24;
@@ -66,16 +67,17 @@ struct LimWs {
   float* scores;        // [B*Q, S_cap]
   uint32_t* slot_table; // [B, kTableStride] token | state << 24
   uint32_t* slot_key;   // [B, kTableStride] score key of candidate slots
-  uint32_t* select;     // [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq, tie cutoff token
-  int32_t* part_counts; // [B, parts, 8] per 4096-token chunk: MTP0 misses, in-bin tokens, then the misses before it; MTP3 misses by first-selecting query, selected per query
-  int32_t* vslot;       // MTP0: [B, 2, kTopK] victim slots, then the token each evicts (-1: free); MTP3: [B, 8192] slots
-  int32_t* nvict;       // [B] victims found
+  int32_t* part_counts; // [B, parts, 8] per 4096-token chunk: MTP0 definite misses, in-bin tokens; MTP3 misses by first-selecting query, selected per query
+  uint32_t* select;     // MTP3: [B*Q, 4] top-2048 threshold key, need_eq, cnt_eq, tie cutoff token
+  int32_t* vslot;       // MTP3: [B, 8192] victim slots
+  int32_t* nvict;       // MTP3: [B] victims found
   uint8_t* masks;       // MTP3: [B, S_cap] per-token query mask
   int32_t* done;        // MTP0: [B] chunks that finished lim_classify_kernel
   uint2* ranges;        // MTP0: [B, S_cap/128] smallest and largest score key of each 128-token block
   uint32_t* hist;       // MTP0: [B, kHistBins] first-digit histogram of the request's keys
-  uint32_t* rowsel;     // MTP0: [B, 4] the request's smallest key, first-digit shift, miss count
+  uint32_t* rowsel;     // MTP0: [B, 4] the request's smallest key and first-digit shift
   uint4* gather;        // MTP0: [B, parts, kGatherPart] each chunk's (token, key, pool slot, -) in the threshold's first-digit bin
+  int32_t* missl;       // MTP0: [B, parts, kMissPart] each chunk's definite misses (selected, not cached), in token order
 };
 
 // Management runs one workgroup per kChunk-token chunk of a request.
@@ -95,11 +97,11 @@ LimWs lim_layout(void* base, int64_t batch, int64_t cap, int queries, size_t* by
   w.scores = reinterpret_cast<float*>(take(sizeof(float) * B * queries * cap));
   w.slot_table = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * kTableStride));
   w.slot_key = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * kTableStride));
-  w.select = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4 * B * queries));
   w.part_counts = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B * mtp_parts(cap) * 8));
-  w.vslot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B * (queries > 1 ? kUnionCap : 2 * kTopK)));
-  w.nvict = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B));
   if (queries > 1) {
+    w.select = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4 * B * queries));
+    w.vslot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B * kUnionCap));
+    w.nvict = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B));
     w.masks = reinterpret_cast<uint8_t*>(take(B * cap));
   } else {
     w.done = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B));
@@ -107,6 +109,7 @@ LimWs lim_layout(void* base, int64_t batch, int64_t cap, int queries, size_t* by
     w.hist = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * kHistBins));
     w.rowsel = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4 * B));
     w.gather = reinterpret_cast<uint4*>(take(sizeof(uint4) * B * mtp_parts(cap) * kGatherPart));
+    w.missl = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * B * mtp_parts(cap) * kMissPart));
   }
   if (bytes != nullptr) *bytes = p - p0;
   return w;
@@ -693,36 +696,40 @@ __device__ inline int tie_cutoff_step(unsigned eqm, int t0, int want, int before
   return before + tot;
 }
 
-// select_victims with the slot states and keys held in registers: thread t
-// owns slots [t*ITEMS, (t+1)*ITEMS) (slot order = thread-major order), read
-// once.  Same result as select_victims; requires c <= ITEMS * kManageThreads
-// and tables readable up to ITEMS * kManageThreads entries.
+// Thread t's slot states and score keys of slots [t*ITEMS, (t+1)*ITEMS), one
+// vector load each (tables readable up to ITEMS * kManageThreads entries).
 template <int ITEMS>
-__device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot,
-                                                   uint32_t* hist, int* scratch, int* bcast, uint32_t* red,
-                                                   int* vevict = nullptr) {
+__device__ __forceinline__ void load_slot_regs(const uint32_t* stab, const uint32_t* skey, uint32_t (&st)[ITEMS],
+                                               uint32_t (&kv)[ITEMS]) {
   static_assert(ITEMS % 4 == 0, "vector loads of four slots");
+  const int i0 = threadIdx.x * ITEMS;
+#pragma unroll
+  for (int j = 0; j < ITEMS / 4; ++j) {
+    const uint4 a = *reinterpret_cast<const uint4*>(stab + i0 + 4 * j);
+    const uint4 b = *reinterpret_cast<const uint4*>(skey + i0 + 4 * j);
+    st[4 * j] = a.x; st[4 * j + 1] = a.y; st[4 * j + 2] = a.z; st[4 * j + 3] = a.w;
+    kv[4 * j] = b.x; kv[4 * j + 1] = b.y; kv[4 * j + 2] = b.z; kv[4 * j + 3] = b.w;
+  }
+}
+
+// select_victims with the slot states and keys held in registers (from
+// load_slot_regs): thread t owns slots [t*ITEMS, (t+1)*ITEMS) (slot order =
+// thread-major order).  Same result as select_victims; requires
+// c <= ITEMS * kManageThreads.
+template <int ITEMS>
+__device__ __forceinline__ int select_victims_in_regs(int c, int m, const uint32_t (&st)[ITEMS],
+                                                      const uint32_t (&kv)[ITEMS], int* vslot, uint32_t* hist,
+                                                      int* scratch, int* bcast, uint32_t* red, int* vevict) {
   const int tid = threadIdx.x;
   if (m <= 0) return 0;
   const int i0 = tid * ITEMS;
   uint32_t key[ITEMS];
-  uint32_t st[ITEMS];
   unsigned nh = 0u;  // non-hit slots (victim candidates) below c
-  {
-    uint32_t kv[ITEMS];
 #pragma unroll
-    for (int j = 0; j < ITEMS / 4; ++j) {
-      const uint4 a = *reinterpret_cast<const uint4*>(stab + i0 + 4 * j);
-      const uint4 b = *reinterpret_cast<const uint4*>(skey + i0 + 4 * j);
-      st[4 * j] = a.x; st[4 * j + 1] = a.y; st[4 * j + 2] = a.z; st[4 * j + 3] = a.w;
-      kv[4 * j] = b.x; kv[4 * j + 1] = b.y; kv[4 * j + 2] = b.z; kv[4 * j + 3] = b.w;
-    }
-#pragma unroll
-    for (int e = 0; e < ITEMS; ++e) {
-      const uint32_t state = st[e] >> kStateShift;
-      key[e] = ~(state == kStateFree ? 0u : kv[e]);  // smallest score = largest inverted key; free slots first
-      if (i0 + e < c && state != kStateHit) nh |= 1u << e;
-    }
+  for (int e = 0; e < ITEMS; ++e) {
+    const uint32_t state = st[e] >> kStateShift;
+    key[e] = ~(state == kStateFree ? 0u : kv[e]);  // smallest score = largest inverted key; free slots first
+    if (i0 + e < c && state != kStateHit) nh |= 1u << e;
   }
   uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
@@ -782,6 +789,16 @@ __device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t*
     }
   __syncthreads();
   return tot < m ? tot : m;
+}
+
+template <int ITEMS>
+__device__ __forceinline__ int select_victims_regs(int c, int m, const uint32_t* stab, const uint32_t* skey, int* vslot,
+                                                   uint32_t* hist, int* scratch, int* bcast, uint32_t* red,
+                                                   int* vevict = nullptr) {
+  if (m <= 0) return 0;
+  uint32_t st[ITEMS], kv[ITEMS];
+  load_slot_regs<ITEMS>(stab, skey, st, kv);
+  return select_victims_in_regs<ITEMS>(c, m, st, kv, vslot, hist, scratch, bcast, red, vevict);
 }
 
 // ---------------------------------------------------------------------------
@@ -907,7 +924,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
 }
 
 // ---------------------------------------------------------------------------
-// 2a. MTP0 management, three chunked kernels after the scores, one 512-thread
+// 2a. MTP0 management, two chunked kernels after the scores, one 512-thread
 // workgroup per 4096-token chunk of a request.  (One workgroup per request
 // keeps every pass over the request's tokens on one CU, where each pass is
 // bound by that CU's vector ALUs: 26 us at 32768 candidates.)
@@ -918,17 +935,14 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
 //   lim_classify  every chunk finds the bin holding the 2048th largest key
 //                 from the histogram and classifies its tokens outside that
 //                 bin (above: selected, below: not): cached tokens go to the
-//                 slot table, misses are counted per chunk, tokens in the bin
-//                 are gathered.  The last chunk of the request to finish (a
-//                 device-scope counter, nobody waits) resolves the threshold
-//                 among the gathered tokens (ties to the lower token),
-//                 classifies them, selects the victims and writes the hit half
-//                 of the output row.
-//   lim_place     every chunk writes its misses after those of the chunks
-//                 before it, paired with the ascending victim slots, and
-//                 updates the pool.
-// The score kernel zeroes each request's histogram, gather count and
-// finished-chunk counter.
+//                 slot table; definite misses (selected, not cached) and the
+//                 tokens in the bin are handed over, in token order, in the
+//                 chunk's slices of two workspace lists.  The last chunk of
+//                 the request to finish (a device-scope counter, nobody
+//                 waits) resolves the threshold among the in-bin tokens (ties
+//                 to the lower token), classifies them, selects the victims,
+//                 and writes the whole output row and the pool update.
+// The score kernel zeroes each request's histogram and finished-chunk counter.
 static_assert(kHistBins == 8 * kManageThreads, "lim_classify: eight first-digit bins per thread");
 static_assert(kChunk == 4096, "the gather list holds one chunk's worth of tokens");
 
@@ -1047,30 +1061,103 @@ __device__ __forceinline__ void write_hit_rows(const LimArgs& a, int b, int c, i
   if (tid == 0) a.miss_counts[b] = m;
 }
 
+// LDS of lim_classify_kernel's last chunk (mtp0_resolve).  `region` holds, in
+// turn, the in-bin ranking lists, the radix histogram of the selects and the
+// ordered miss list.
+struct ResolveLds {
+  uint32_t* region;   // kBins words
+  int* scratch;
+  uint64_t* scratch64;
+  uint32_t* red;
+  int* bcast;
+  int* cdm;    // [active] definite misses of each chunk
+  int* cim;    // [active] in-bin misses of each chunk
+  int* doff;   // [active] offset of each chunk's definite misses in dmiss
+  int* goff;   // [active] offset of each chunk's in-bin tokens, then the misses before each chunk
+  int* dmiss;  // [kTopK] definite misses, chunk by chunk (each in token order)
+  int* ibm;    // [kTopK] in-bin misses, any order
+  int* nibm;
+  int* vsl;    // [kTopK] victim slots
+  int* vev;    // [kTopK] token each victim evicts, or -1
+};
+
+// Last chunk p with off[p] <= f among chunks [0, active) (off ascending).
+__device__ inline int chunk_of(const int* off, int active, int f) {
+  int lo_p = 0, hi_p = active - 1;
+  while (lo_p < hi_p) {
+    const int mid = (lo_p + hi_p + 1) >> 1;
+    if (off[mid] <= f) lo_p = mid;
+    else hi_p = mid - 1;
+  }
+  return lo_p;
+}
+
 // The last chunk of a request in lim_classify_kernel: the threshold among the
 // tokens of the first-digit bin `bin` (the k-th largest of them is the
-// request's 2048th largest key), their classification and the victims.
-// counts[p * 8] holds chunk p's miss count, counts[p * 8 + 1] its in-bin
-// token count (its slice of the gather list holds the first kGatherPart);
-// counts[p * 8 + 2] gets the misses of the chunks before p.
+// request's 2048th largest key), their classification, the victims, and the
+// whole output row with the pool update.  counts[p * 8] holds chunk p's
+// definite-miss count, counts[p * 8 + 1] its in-bin token count; its slices
+// of the hand-over lists hold the first kMissPart / kGatherPart of them.
 __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, int b, int n, int c, int r, int parts,
                                              int active, uint32_t bin, int k, uint32_t lo, int shift,
-                                             uint32_t* hist, int* scratch, uint32_t* red, int* bcast, int* pcount,
-                                             int* goff, uint32_t* lkey, int* ltok) {
+                                             const ResolveLds& L) {
   const int tid = threadIdx.x;
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + static_cast<int64_t>(b) * cap;
-  const int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
+  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
   uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
   uint32_t* skey = w.slot_key + static_cast<int64_t>(b) * kTableStride;
-  int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
-  // Chunk counts (active <= kManageThreads: one chunk per thread).
-  const int my_in = tid < active ? counts[tid * 8 + 1] : 0;
-  if (tid < active) pcount[tid] = counts[tid * 8];
-  int g;
-  const int off = block_exclusive_scan(min(my_in, kGatherPart), scratch, &g);
-  const bool overflow = __syncthreads_or(my_in > kGatherPart) != 0;
-  if (tid < active) goff[tid] = off;  // ordered before its reads by the barriers below
+  const int32_t* counts = w.part_counts + static_cast<int64_t>(b) * parts * 8;
+  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
+  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
+
+  // 1. Chunk counts (active <= kManageThreads: one chunk per thread) and the
+  //    offsets of the chunks' hand-over slices.
+  int dm = 0, ni = 0;
+  if (tid < active) {
+    dm = counts[tid * 8];
+    ni = counts[tid * 8 + 1];
+    L.cdm[tid] = dm;
+    L.cim[tid] = 0;
+  }
+  if (tid == 0) *L.nibm = 0;
+  uint64_t tot2;
+  const uint64_t ex = block_exclusive_scan4(static_cast<uint64_t>(min(dm, kMissPart)) << 32 |
+                                                static_cast<uint64_t>(min(ni, kGatherPart)),
+                                            L.scratch64, &tot2);
+  const int nd = static_cast<int>(tot2 >> 32);          // definite misses handed over
+  const int g = static_cast<int>(tot2 & 0xffffffffu);   // in-bin tokens handed over
+  if (tid < active) {
+    L.doff[tid] = static_cast<int>(ex >> 32);
+    L.goff[tid] = static_cast<int>(ex & 0xffffffffu);
+  }
+  const bool gather_over = __syncthreads_or(ni > kGatherPart) != 0;
+  const bool miss_over = __syncthreads_or(dm > kMissPart) != 0;  // these barriers also publish doff / goff
+
+  // 2. The handed-over definite misses, and the in-bin tokens for the ranking.
+  for (int f = tid; f < nd; f += kManageThreads) {
+    const int p = chunk_of(L.doff, active, f);
+    L.dmiss[f] = w.missl[(static_cast<int64_t>(b) * parts + p) * kMissPart + (f - L.doff[p])];
+  }
+  const bool direct = !gather_over && g <= kRankDirect;
+  uint32_t* lkey = L.region;
+  int* ltok = reinterpret_cast<int*>(L.region + kRankDirect);
+  int my_t = 0;
+  uint32_t my_k = 0u;
+  int32_t my_slot = -1;
+  if (direct && tid < g) {
+    const int p = chunk_of(L.goff, active, tid);
+    const uint4 e = w.gather[(static_cast<int64_t>(b) * parts + p) * kGatherPart + (tid - L.goff[p])];
+    my_t = static_cast<int>(e.x);
+    my_k = e.y;
+    my_slot = static_cast<int32_t>(e.z);
+    ltok[tid] = my_t;
+    lkey[tid] = my_k;
+  }
+  __syncthreads();
+
+  // 3. The threshold among the in-bin tokens (ties go to the lower token) and
+  //    their classification: cached ones into the slot table, misses listed.
   uint32_t thr = 0u;
   int cutoff = INT_MAX;
   auto classify = [&](int t, int32_t slot, bool selected, uint32_t key) {
@@ -1082,32 +1169,12 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
         skey[slot] = key;
       }
     } else if (selected) {
-      atomicAdd(&pcount[t / kChunk], 1);
+      atomicAdd(&L.cim[t / kChunk], 1);
+      L.ibm[atomicAdd(L.nibm, 1)] = t;  // at most k <= kTopK in-bin tokens are selected
     }
   };
-  if (!overflow && g <= kRankDirect) {
-    // Few tokens in the bin: gather them into LDS and rank them pairwise
-    // (key descending, then token ascending: ties go to the lower token).
-    // Entry f of the list comes from the last chunk p with goff[p] <= f.
-    __syncthreads();  // goff
-    int my_t = 0;
-    uint32_t my_k = 0u;
-    int32_t my_slot = -1;
-    if (tid < g) {
-      int lo_p = 0, hi_p = active - 1;
-      while (lo_p < hi_p) {
-        const int mid = (lo_p + hi_p + 1) >> 1;
-        if (goff[mid] <= tid) lo_p = mid;
-        else hi_p = mid - 1;
-      }
-      const uint4 e = w.gather[(static_cast<int64_t>(b) * parts + lo_p) * kGatherPart + (tid - goff[lo_p])];
-      my_t = static_cast<int>(e.x);
-      my_k = e.y;
-      my_slot = static_cast<int32_t>(e.z);
-      ltok[tid] = my_t;
-      lkey[tid] = my_k;
-    }
-    __syncthreads();
+  if (direct) {
+    // Rank pairwise: key descending, then token ascending.
     if (tid < g) {
       int rank = 0;
       for (int j = 0; j < g; ++j) {
@@ -1115,17 +1182,18 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
         rank += (kj > my_k || (kj == my_k && ltok[j] < my_t)) ? 1 : 0;
       }
       if (rank == k - 1) {  // the last selected token: the threshold and the tie cutoff
-        bcast[0] = static_cast<int>(my_k);
-        bcast[1] = my_t;
+        L.bcast[0] = static_cast<int>(my_k);
+        L.bcast[1] = my_t;
       }
       classify(my_t, my_slot, rank < k, my_k);
     }
     __syncthreads();
-    thr = static_cast<uint32_t>(bcast[0]);
-    cutoff = bcast[1];
+    thr = static_cast<uint32_t>(L.bcast[0]);
+    cutoff = L.bcast[1];
   } else {
-    // More tokens in the bin than the lists hold (heavy ties, or a key range
+    // More in-bin tokens than the lists hold (heavy ties, or a key range
     // stretched by unmapped index blocks): stream the request's scores.
+    uint32_t* hist = L.region;
     for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
     __syncthreads();
     const uint32_t klo = lo + (bin << shift);  // keys in the bin lie in [klo, khi]
@@ -1137,7 +1205,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
 #pragma unroll
       for (int e = 0; e < 4; ++e) inc[e] = inc[e] && ((key[e] - lo) >> shift) == bin;
     };
-    const SelectOut sel = radix_select(ngroups, k, klo, khi, load_bin, hist, scratch, bcast);
+    const SelectOut sel = radix_select(ngroups, k, klo, khi, load_bin, hist, L.scratch, L.bcast);
     thr = sel.thresh;
     if (sel.need_eq != sel.cnt_eq) {  // ties at the threshold: one ordered pass finds the last selected
       int before = 0;
@@ -1152,10 +1220,10 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
           for (int e = 0; e < 4; ++e)
             if (inc[e] && key[e] == thr) eqm |= 1u << e;
         }
-        before = tie_cutoff_step(eqm, 4 * gi, sel.need_eq - 1, before, scratch, bcast);
+        before = tie_cutoff_step(eqm, 4 * gi, sel.need_eq - 1, before, L.scratch, L.bcast);
       }
       __syncthreads();
-      cutoff = bcast[3];
+      cutoff = L.bcast[3];
     }
     for (int gi = tid; gi < ngroups; gi += kManageThreads) {
       uint32_t key[4];
@@ -1166,40 +1234,144 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
         if (inc[e]) classify(4 * gi + e, pool[4 * gi + e], mtp0_selected(key[e], 4 * gi + e, thr, cutoff), key[e]);
     }
   }
-  if (tid == 0) {
-    uint32_t* out = w.select + static_cast<int64_t>(b) * 4;
-    out[0] = thr;
-    out[3] = static_cast<uint32_t>(cutoff);
-  }
-  __syncthreads();  // the slot table and the chunk counts are complete
-  const int mine = tid < active ? pcount[tid] : 0;
-  int total;
-  const int before = block_exclusive_scan(mine, scratch, &total);
-  if (tid < active) counts[tid * 8 + 2] = before;
-  const int m = min(total, kTopK);  // misses are selected tokens
-  if (tid == 0) w.rowsel[4 * b + 2] = static_cast<uint32_t>(m);
+  __syncthreads();  // the slot table, cim and the in-bin miss list are complete
+
+  // 4. Misses per chunk, their bases, and the victims.
+  const int mine = tid < active ? L.cdm[tid] + L.cim[tid] : 0;
+  int m_all;
+  const int base = block_exclusive_scan(mine, L.scratch, &m_all);
+  if (tid < active) L.goff[tid] = base;  // goff now holds the misses before each chunk
+  const int m = min(m_all, kTopK);       // misses are selected tokens
+  const int nib = *L.nibm;
+  uint32_t* hist = L.region;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   __syncthreads();
-  // Budgets up to 2048 slots hold the slot states in registers (4 per thread);
-  // larger ones stream them (a 16-per-thread variant here costs the kernel
-  // its second workgroup per CU: 144 instead of 116 VGPRs).
-  int32_t* vslot = w.vslot + static_cast<int64_t>(b) * 2 * kTopK;
-  const int nv = c <= 4 * kManageThreads
-                     ? select_victims_regs<4>(c, m, stab, skey, vslot, hist, scratch, bcast, red, vslot + kTopK)
-                     : select_victims(c, m, stab, skey, vslot, hist, scratch, bcast, red, vslot + kTopK);
-  if (tid == 0) w.nvict[b] = nv;
+  constexpr int kSlotRegs = 4;  // budgets up to kSlotRegs * kManageThreads slots keep their states in registers
+  const bool slots_in_regs = c <= kSlotRegs * kManageThreads;
+  uint32_t st[kSlotRegs], kv[kSlotRegs];
+  int nv;
+  if (slots_in_regs) {
+    load_slot_regs<kSlotRegs>(stab, skey, st, kv);
+    nv = select_victims_in_regs<kSlotRegs>(c, m, st, kv, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+  } else {
+    nv = select_victims(c, m, stab, skey, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+  }
+  __syncthreads();  // the histogram is free again
+
+  // 5. The ordered miss list (ascending token): a chunk's definite misses and
+  //    in-bin misses interleave by token; chunks follow one another.
+  int* misstok = reinterpret_cast<int*>(L.region);
+  for (int f = tid; f < nd; f += kManageThreads) {
+    const int p = chunk_of(L.doff, active, f);
+    if (L.cdm[p] > kMissPart) continue;  // placed by the ordered pass below
+    const int t = L.dmiss[f];
+    int before_ib = 0;
+    for (int j = 0; j < nib; ++j) {
+      const int x = L.ibm[j];
+      before_ib += (x < t && x >= p * kChunk) ? 1 : 0;
+    }
+    const int pos = L.goff[p] + (f - L.doff[p]) + before_ib;
+    if (pos < kTopK) misstok[pos] = t;
+  }
+  for (int j = tid; j < nib; j += kManageThreads) {
+    const int t = L.ibm[j];
+    const int p = t / kChunk;
+    if (L.cdm[p] > kMissPart) continue;
+    // Definite misses of chunk p below t: binary search of its sorted slice.
+    int lo_i = L.doff[p], hi_i = L.doff[p] + L.cdm[p];
+    while (lo_i < hi_i) {
+      const int mid = (lo_i + hi_i) >> 1;
+      if (L.dmiss[mid] < t) lo_i = mid + 1;
+      else hi_i = mid;
+    }
+    int before_ib = 0;
+    for (int j2 = 0; j2 < nib; ++j2) {
+      const int x = L.ibm[j2];
+      before_ib += (x < t && x >= p * kChunk) ? 1 : 0;
+    }
+    const int pos = L.goff[p] + (lo_i - L.doff[p]) + before_ib;
+    if (pos < kTopK) misstok[pos] = t;
+  }
+  if (miss_over) {
+    // Chunks with more definite misses than their slice: one ordered pass
+    // over the chunk's tokens (the pool is not updated yet).
+    for (int p = 0; p < active; ++p) {
+      if (L.cdm[p] <= kMissPart) continue;  // uniform
+      const int t0 = p * kChunk + tid * kItems;
+      uint32_t u[kItems];
+      int32_t slot[kItems];
+      bool in[kItems];
+      load_tokens8(s, pool, n, t0, u, slot, in);
+      unsigned missm = 0u;
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (in[e] && mtp0_selected(u[e], t0 + e, thr, cutoff) && !(slot[e] >= 0 && slot[e] < c)) missm |= 1u << e;
+      int tot;
+      int pos = L.goff[p] + block_exclusive_scan(__popc(missm), L.scratch, &tot);
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if ((missm >> e) & 1u) {
+          if (pos < kTopK) misstok[pos] = t0 + e;
+          ++pos;
+        }
+    }
+  }
+  __syncthreads();
+
+  // 6. Misses first (ascending token) paired with the ascending victim slots,
+  //    and the pool update.
+  for (int pos = tid; pos < m; pos += kManageThreads) {
+    const int t = misstok[pos];
+    const int d = pos < nv ? L.vsl[pos] : -1;
+    const int evicted = pos < nv ? L.vev[pos] : -1;  // an unselected token, or -1 for a free slot
+    out_src[pos] = t;
+    out_dst[pos] = d;
+    if (d >= 0) {
+      if (evicted >= 0) pool[evicted] = -1;
+      pool[t] = d;
+    }
+  }
+
+  // 7. Then the hits by descending old slot (reference BuildHitMissKey order).
+  if (!slots_in_regs) {
+    write_hit_rows(a, b, c, m, stab, L.scratch);
+    return;
+  }
+  const int i0 = tid * kSlotRegs;
+  unsigned hm = 0u;
+#pragma unroll
+  for (int e = 0; e < kSlotRegs; ++e)
+    if (i0 + e < c && (st[e] >> kStateShift) == kStateHit) hm |= 1u << e;
+  int nhits;
+  const int below = block_exclusive_scan(__popc(hm), L.scratch, &nhits);  // hits in lower slots
+  int above = nhits - below - __popc(hm);                                  // hits in higher slots
+#pragma unroll
+  for (int e = kSlotRegs - 1; e >= 0; --e)
+    if ((hm >> e) & 1u) {
+      const int pos = m + above;
+      if (pos < kTopK) {
+        out_src[pos] = static_cast<int32_t>(st[e] & kTokenMask);
+        out_dst[pos] = i0 + e;
+      }
+      ++above;
+    }
+  // Positions a corrupt pool (duplicate slots) left unfilled.
+  for (int pos = m + nhits + tid; pos < kTopK; pos += kManageThreads) {
+    out_src[pos] = -1;
+    out_dst[pos] = -1;
+  }
+  if (tid == 0) a.miss_counts[b] = m;
 }
 
 __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a, LimWs w, int parts) {
-  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t region[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
-  __shared__ int pcount[kManageThreads];
-  __shared__ int goff[kManageThreads];
-  __shared__ uint32_t lkey[kRankDirect];
-  __shared__ int ltok[kRankDirect];
+  __shared__ int cdm[kManageThreads], cim[kManageThreads], doff[kManageThreads], goff[kManageThreads];
+  __shared__ int dmiss[kTopK], ibm[kTopK], vsl[kTopK], vev[kTopK];
+  __shared__ int nibm;
   __shared__ int last;
   const int b = blockIdx.x / parts;
   const int part = blockIdx.x - b * parts;
@@ -1272,17 +1444,25 @@ __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a,
       missm |= 1u << e;
     }
   }
-  // One scan for both counts (each below 2^16): misses high, in-bin tokens low.
+  // One scan for both counts (each below 2^16): definite misses high, in-bin
+  // tokens low; both hand-over slices keep token order.
   uint64_t tot;
   const uint64_t pos = block_exclusive_scan4(static_cast<uint64_t>(__popc(missm)) << 16 | __popc(inbin), scratch64, &tot);
-  int idx = static_cast<int>(pos & 0xffffu);
+  int midx = static_cast<int>((pos >> 16) & 0xffffu);
+  int iidx = static_cast<int>(pos & 0xffffu);
+  int32_t* ml = w.missl + (static_cast<int64_t>(b) * parts + part) * kMissPart;
   uint4* gl = w.gather + (static_cast<int64_t>(b) * parts + part) * kGatherPart;
 #pragma unroll
-  for (int e = 0; e < kItems; ++e)
-    if ((inbin >> e) & 1u) {
-      if (idx < kGatherPart) gl[idx] = make_uint4(static_cast<uint32_t>(t0 + e), u[e], static_cast<uint32_t>(slot[e]), 0u);
-      ++idx;
+  for (int e = 0; e < kItems; ++e) {
+    if ((missm >> e) & 1u) {
+      if (midx < kMissPart) ml[midx] = t0 + e;
+      ++midx;
     }
+    if ((inbin >> e) & 1u) {
+      if (iidx < kGatherPart) gl[iidx] = make_uint4(static_cast<uint32_t>(t0 + e), u[e], static_cast<uint32_t>(slot[e]), 0u);
+      ++iidx;
+    }
+  }
   int32_t* counts = w.part_counts + (static_cast<int64_t>(b) * parts + part) * 8;
   if (tid == 0) {
     counts[0] = static_cast<int>((tot >> 16) & 0xffffu);
@@ -1301,70 +1481,8 @@ __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a,
   }
   __syncthreads();
   if (!last) return;
-  mtp0_resolve(a, w, b, n, c, r, parts, active, static_cast<uint32_t>(bin), kTopK - above, lo, shift, hist, scratch,
-               red, bcast, pcount, goff, lkey, ltok);
-}
-
-// Every chunk writes its misses after those of the chunks before it, paired
-// with the ascending victim slots, and updates the pool; one more workgroup
-// per request (part == parts) writes the hit half of the output row.  Pool
-// entries are read only of selected tokens: evictions rewrite entries of
-// unselected tokens only, and a miss's entry only its own chunk.
-__global__ __launch_bounds__(kManageThreads) void lim_place_kernel(LimArgs a, LimWs w, int parts) {
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  const int b = blockIdx.x / (parts + 1);
-  const int part = blockIdx.x - b * (parts + 1);
-  const int tid = threadIdx.x;
-  const int n = a.num_candidates[b];
-  const int c = a.num_cache[b];
-  const int r = a.pool_entries[b];
-  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows)) return;
-  const uint32_t* stab = w.slot_table + static_cast<int64_t>(b) * kTableStride;
-  if (part == parts) {
-    write_hit_rows(a, b, c, static_cast<int>(w.rowsel[4 * b + 2]), stab, scratch);
-    return;
-  }
-  if (part * kChunk >= n) return;
-  const int64_t cap = a.source_capacity;
-  int32_t* pool = a.pool + static_cast<int64_t>(r) * cap;
-  // Every load that does not depend on another is issued first.
-  const int before = w.part_counts[(static_cast<int64_t>(b) * parts + part) * 8 + 2];  // misses of earlier chunks
-  const uint32_t* sel = w.select + static_cast<int64_t>(b) * 4;
-  const uint32_t thr = sel[0];
-  const int cutoff = static_cast<int>(sel[3]);
-  const int nv = w.nvict[b];
-  const int t0 = part * kChunk + tid * kItems;
-  uint32_t u[kItems];
-  int32_t slot[kItems];
-  bool in[kItems];
-  load_tokens8(w.scores + static_cast<int64_t>(b) * cap, pool, n, t0, u, slot, in);
-  const int32_t* vslot = w.vslot + static_cast<int64_t>(b) * 2 * kTopK;
-  const int32_t* vevict = vslot + kTopK;
-  int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
-  int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
-  // Only selected tokens' slots are used: their entries are this chunk's alone.
-  unsigned missm = 0u;
-#pragma unroll
-  for (int e = 0; e < kItems; ++e)
-    if (in[e] && mtp0_selected(u[e], t0 + e, thr, cutoff) && !(slot[e] >= 0 && slot[e] < c)) missm |= 1u << e;
-  int tot;
-  int pos = before + block_exclusive_scan(__popc(missm), scratch, &tot);
-#pragma unroll
-  for (int e = 0; e < kItems; ++e) {
-    if (!((missm >> e) & 1u)) continue;
-    const int t = t0 + e;
-    const int d = pos < nv ? vslot[pos] : -1;
-    const int evicted = pos < nv ? vevict[pos] : -1;  // an unselected token, or -1 for a free slot
-    if (pos < kTopK) {
-      out_src[pos] = t;
-      out_dst[pos] = d;
-    }
-    if (d >= 0) {
-      if (evicted >= 0) pool[evicted] = -1;
-      pool[t] = d;
-    }
-    ++pos;
-  }
+  const ResolveLds L{region, scratch, scratch64, red, bcast, cdm, cim, doff, goff, dmiss, ibm, &nibm, vsl, vev};
+  mtp0_resolve(a, w, b, n, c, r, parts, active, static_cast<uint32_t>(bin), kTopK - above, lo, shift, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -1810,8 +1928,6 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   if (Q == 1) {
     launch_kernel(kKernLimHist, lim_hist_kernel, pgrid, mblock, stream, a, w, parts);
     launch_kernel(kKernLimClassify, lim_classify_kernel, pgrid, mblock, stream, a, w, parts);
-    launch_kernel(kKernLimPlace, lim_place_kernel, dim3(static_cast<uint32_t>(a.batch * (parts + 1))), mblock, stream,
-                  a, w, parts);
     return hipGetLastError();
   }
   // MTP3: thresholds first, one workgroup per (request, query) score row.

@@ -31,8 +31,7 @@ enum KernelId : int {
   kKernIdxRope = 15,
   kKernPersist = 16,
   kKernLimClassify = 17,
-  kKernLimPlace = 18,
-  kKernCount = 19
+  kKernCount = 18
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.

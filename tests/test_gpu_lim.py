@@ -130,6 +130,28 @@ def test_lim_closed_form_and_repeat(heads, batch, seq_len, cache_tokens, miss):
     _validate(d, pool1, seq_len, cache_tokens, 0)
 
 
+@pytest.mark.parametrize("n_tokens,cache_tokens", [(12288, 2048), (20480, 6144)])
+def test_lim_cold_pool_rows_bit_exact(n_tokens, cache_tokens):
+    """Pool rows with nothing cached (every selected token a miss, every
+    victim a free slot) beside a warm row: each chunk hands over far more
+    misses than its slice holds, so the last chunk re-derives their order;
+    every output and the pool bit-exact, and the repeat call has no misses."""
+    from nanovllm_amd.workloads import make_chain_case
+
+    case = make_chain_case(3, n_tokens, cache_tokens, [7, 30, 90], seed=29)
+    t = case.tensors
+    for row in ints(t["req_pool_entries"])[:2]:
+        t["cache_slots_pool"][int(row)].fill_(-1)
+    print(f"LIM cold pool rows N={n_tokens} C={cache_tokens}", flush=True)
+    expect = oracle_lim(case)
+    assert (expect["miss_counts"][:2] == 2048).all() and expect["miss_counts"][2] < 2048
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d)
+    _assert_matches(d, expect, False)
+    _run_lim(d)
+    assert (ints(d["miss_counts"]) == 0).all()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("heads", [32, 64])
 def test_lim_random_bit_exact(dtype, heads):
