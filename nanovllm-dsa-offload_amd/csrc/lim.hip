@@ -53,6 +53,9 @@ constexpr int kHistBins = 1 << kHistBits;
 constexpr int kGatherPart = 128;                  // MTP0: in-bin tokens a chunk can hand over
 constexpr int kRankDirect = 512;                  // MTP0: in-bin tokens ranked pairwise by the last chunk
 constexpr int kMissPart = 256;                    // MTP0: definite misses a chunk can hand over
+constexpr int kSpecChunks = 16;                   // MTP0 last chunk: requests of up to this many chunks ...
+constexpr int kSpecEntries = 64;                  // ... read this many definite misses per chunk up front
+constexpr int kSpecGather = 16;                   // ... and this many in-bin tokens
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr int kTableStride = kSlotStride + kManageThreads;  // workspace slot tables: + one junk word per thread
 constexpr uint32_t kStateShift = 24;
@@ -320,7 +323,10 @@ struct SelectOut {
   int cnt_eq;       // elements equal to thresh (INT_MAX when not counted)
 };
 
-// Block-wide min / max of 32-bit keys (every thread gets the result).
+// Block-wide min / max of 32-bit keys (every thread gets the result; every
+// thread reads the wave results itself).  LDS_ONLY: barriers that order LDS
+// only.
+template <bool LDS_ONLY = false>
 __device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
@@ -333,21 +339,19 @@ __device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
     red[2 * wid] = lo;
     red[2 * wid + 1] = hi;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t l = red[0], h = red[1];
-    for (int w = 1; w < nw; ++w) {
+  scan_barrier<LDS_ONLY>();
+  uint32_t l = 0xffffffffu, h = 0u;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    if (w < nw) {
       l = min(l, red[2 * w]);
       h = max(h, red[2 * w + 1]);
     }
-    red[2 * nw] = l;
-    red[2 * nw + 1] = h;
   }
-  __syncthreads();
   // Uniform values (readfirstlane): they steer loops that contain barriers.
-  lo = __builtin_amdgcn_readfirstlane(red[2 * nw]);
-  hi = __builtin_amdgcn_readfirstlane(red[2 * nw + 1]);
-  __syncthreads();
+  lo = __builtin_amdgcn_readfirstlane(l);
+  hi = __builtin_amdgcn_readfirstlane(h);
+  scan_barrier<LDS_ONLY>();  // red is reused
 }
 
 // k-th largest key among included keys, all of which lie in [kmin, kmax].
@@ -461,14 +465,31 @@ __device__ SelectOut radix_select(int ngroups, int k, uint32_t kmin, uint32_t km
       hist, scratch, bcast);
 }
 
+// Bitwise OR of one word per thread over the workgroup, with barriers that
+// order LDS only.  `scratch` must hold blockDim/64 ints.
+__device__ inline unsigned block_or_lds(unsigned v, int* scratch) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v |= static_cast<unsigned>(__shfl_xor(static_cast<int>(v), d, 64));
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = static_cast<int>(v);
+  lds_barrier();
+  unsigned r = 0u;
+  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) r |= static_cast<unsigned>(scratch[w]);
+  lds_barrier();
+  return __builtin_amdgcn_readfirstlane(r);
+}
+
+template <bool LDS_ONLY = false>
 __device__ inline int block_sum(int v, int* scratch) {
   int total;
-  (void)block_exclusive_scan(v, scratch, &total);
+  (void)block_exclusive_scan<LDS_ONLY>(v, scratch, &total);
   return total;
 }
 
 // Exclusive block scan of four packed 16-bit counters (each chunk total must
-// stay below 65536: at most kChunk per chunk here).
+// stay below 65536: at most kChunk per chunk here), or of any packed fields
+// whose block totals fit their widths.  LDS_ONLY: barriers that order LDS
+// only (global accesses in flight stay in flight).
+template <bool LDS_ONLY = false>
 __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, uint64_t* total) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -481,23 +502,20 @@ __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, 
     if (lane >= d) x += (static_cast<uint64_t>(hi) << 32) | lo;
   }
   if (lane == 63) scratch[wid] = x;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t run = 0;
-    for (int w = 0; w < nw; ++w) {
+  scan_barrier<LDS_ONLY>();
+  uint64_t before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    if (w < nw) {  // every thread reads the wave totals
       const uint64_t t = scratch[w];
-      scratch[w] = run;
-      run += t;
+      before += w < wid ? t : 0;
+      tot += t;
     }
-    scratch[nw] = run;
   }
-  __syncthreads();
-  const uint64_t excl = scratch[wid] + x - v;
-  const uint64_t t = scratch[nw];
-  *total = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t >> 32))) << 32) |
-           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t)));
-  __syncthreads();
-  return excl;
+  *total = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tot >> 32))) << 32) |
+           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tot)));
+  scan_barrier<LDS_ONLY>();  // scratch is reused by the next scan
+  return before + x - v;
 }
 
 __device__ inline int lane16(uint64_t v, int q) { return static_cast<int>((v >> (16 * q)) & 0xffffu); }
@@ -716,7 +734,7 @@ __device__ __forceinline__ void load_slot_regs(const uint32_t* stab, const uint3
 // load_slot_regs): thread t owns slots [t*ITEMS, (t+1)*ITEMS) (slot order =
 // thread-major order).  Same result as select_victims; requires
 // c <= ITEMS * kManageThreads.
-template <int ITEMS>
+template <int ITEMS, bool LDS_ONLY = false>
 __device__ __forceinline__ int select_victims_in_regs(int c, int m, const uint32_t (&st)[ITEMS],
                                                       const uint32_t (&kv)[ITEMS], int* vslot, uint32_t* hist,
                                                       int* scratch, int* bcast, uint32_t* red, int* vevict) {
@@ -738,7 +756,7 @@ __device__ __forceinline__ int select_victims_in_regs(int c, int m, const uint32
       lo = min(lo, key[e]);
       hi = max(hi, key[e]);
     }
-  const int nonhit = block_sum(__popc(nh), scratch);
+  const int nonhit = block_sum<LDS_ONLY>(__popc(nh), scratch);
   const bool take_all = m >= nonhit;
   SelectOut sel{0, 0, 0};
   if (!take_all) {
@@ -764,7 +782,7 @@ __device__ __forceinline__ int select_victims_in_regs(int c, int m, const uint32
       }
     if (sel.cnt_eq != sel.need_eq) {  // ties at the threshold: lowest slots first
       int tot;
-      int r = block_exclusive_scan(__popc(eqmask), scratch, &tot);
+      int r = block_exclusive_scan<LDS_ONLY>(__popc(eqmask), scratch, &tot);
 #pragma unroll
       for (int e = 0; e < ITEMS; ++e)
         if ((eqmask >> e) & 1u) {
@@ -776,7 +794,7 @@ __device__ __forceinline__ int select_victims_in_regs(int c, int m, const uint32
     }
   }
   int tot;
-  int pos = block_exclusive_scan(__popc(vmask), scratch, &tot);
+  int pos = block_exclusive_scan<LDS_ONLY>(__popc(vmask), scratch, &tot);
 #pragma unroll
   for (int e = 0; e < ITEMS; ++e)
     if ((vmask >> e) & 1u) {
@@ -787,7 +805,7 @@ __device__ __forceinline__ int select_victims_in_regs(int c, int m, const uint32
       }
       ++pos;
     }
-  __syncthreads();
+  scan_barrier<LDS_ONLY>();
   return tot < m ? tot : m;
 }
 
@@ -1002,7 +1020,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_hist_kernel(LimArgs a, Lim
     hi = max(hi, v.y);
   }
   for (int i = tid; i < kHistBins; i += kManageThreads) hist[i] = 0u;
-  block_minmax(lo, hi, red);  // its barriers also order the clearing before the counts
+  block_minmax<true>(lo, hi, red);  // its barriers also order the clearing before the counts (the key loads stay in flight)
   const int shift = hist_shift(lo, hi);
   if (part == 0 && tid == 0) {
     w.rowsel[4 * b] = lo;
@@ -1111,62 +1129,133 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   int32_t* out_src = a.topk_src + static_cast<int64_t>(b) * kTopK;
   int32_t* out_dst = a.topk_dst + static_cast<int64_t>(b) * kTopK;
 
-  // 1. Chunk counts (active <= kManageThreads: one chunk per thread) and the
-  //    offsets of the chunks' hand-over slices.
-  int dm = 0, ni = 0;
-  if (tid < active) {
-    dm = counts[tid * 8];
-    ni = counts[tid * 8 + 1];
-    L.cdm[tid] = dm;
-    L.cim[tid] = 0;
+  // 1. One round trip: the chunk counts (active <= kManageThreads: one chunk
+  //    per thread), the first entries of every chunk's hand-over slices (when
+  //    active <= kSpecChunks: 32 threads per chunk), and the slot states and
+  //    keys the victims are chosen from.  Everything lands in LDS at once (the
+  //    in-bin tokens then update their slots there), so no register holds it
+  //    across the scans.
+  constexpr int kSlotRegs = 4;  // budgets up to kSlotRegs * kManageThreads slots keep their states in registers
+  const bool slots_in_regs = c <= kSlotRegs * kManageThreads;
+  const bool spec = active <= kSpecChunks;
+  const int sp = tid >> 5, si = tid & 31;
+  uint32_t* lkey = L.region;
+  int* ltok = reinterpret_cast<int*>(L.region + kRankDirect);
+  int* lslot = reinterpret_cast<int*>(L.region + 2 * kRankDirect);
+  uint32_t* lst = L.region + 4 * kRankDirect;                           // [kSlotRegs * kManageThreads] slot states
+  uint32_t* lkv = lst + kSlotRegs * kManageThreads;                      // and keys
+  int* smiss = reinterpret_cast<int*>(lkv + kSlotRegs * kManageThreads);  // [kSpecChunks][kSpecEntries]
+  uint32_t* sgat = reinterpret_cast<uint32_t*>(smiss + kSpecChunks * kSpecEntries);  // [kSpecChunks][kSpecGather][3]
+  static_assert(4 * kRankDirect + 2 * kSlotRegs * kManageThreads + kSpecChunks * (kSpecEntries + 3 * kSpecGather) <=
+                    kBins, "resolve LDS region");
+  {
+    int dm = 0, ni = 0;
+    if (tid < active) {
+      dm = counts[tid * 8];
+      ni = counts[tid * 8 + 1];
+    }
+    int32_t sm[2] = {-1, -1};
+    uint4 sg = make_uint4(0, 0, 0, 0);
+    if (spec && sp < active) {
+      const int32_t* ml = w.missl + (static_cast<int64_t>(b) * parts + sp) * kMissPart;
+      sm[0] = ml[si];
+      sm[1] = ml[si + 32];
+      if (si < kSpecGather) sg = w.gather[(static_cast<int64_t>(b) * parts + sp) * kGatherPart + si];
+    }
+    uint32_t st[kSlotRegs], kv[kSlotRegs];
+    if (slots_in_regs) load_slot_regs<kSlotRegs>(stab, skey, st, kv);
+    if (tid < active) {
+      L.cdm[tid] = dm;
+      L.cim[tid] = ni;  // in-bin count for now; the in-bin miss count below
+    }
+    if (spec && sp < active) {
+      smiss[sp * kSpecEntries + si] = sm[0];
+      smiss[sp * kSpecEntries + si + 32] = sm[1];
+      if (si < kSpecGather) {
+        uint32_t* d = sgat + (sp * kSpecGather + si) * 3;
+        d[0] = sg.x;
+        d[1] = sg.y;
+        d[2] = sg.z;
+      }
+    }
+    if (slots_in_regs) {
+#pragma unroll
+      for (int e = 0; e < kSlotRegs; ++e) {
+        lst[tid * kSlotRegs + e] = st[e];
+        lkv[tid * kSlotRegs + e] = kv[e];
+      }
+    }
   }
   if (tid == 0) *L.nibm = 0;
+  const int dm = tid < active ? L.cdm[tid] : 0;  // (the thread's own store)
+  const int ni = tid < active ? L.cim[tid] : 0;
   uint64_t tot2;
-  const uint64_t ex = block_exclusive_scan4(static_cast<uint64_t>(min(dm, kMissPart)) << 32 |
-                                                static_cast<uint64_t>(min(ni, kGatherPart)),
-                                            L.scratch64, &tot2);
+  const uint64_t ex = block_exclusive_scan4<true>(static_cast<uint64_t>(min(dm, kMissPart)) << 32 |
+                                                      static_cast<uint64_t>(min(ni, kGatherPart)),
+                                                  L.scratch64, &tot2);
   const int nd = static_cast<int>(tot2 >> 32);          // definite misses handed over
   const int g = static_cast<int>(tot2 & 0xffffffffu);   // in-bin tokens handed over
   if (tid < active) {
     L.doff[tid] = static_cast<int>(ex >> 32);
     L.goff[tid] = static_cast<int>(ex & 0xffffffffu);
   }
-  const bool gather_over = __syncthreads_or(ni > kGatherPart) != 0;
-  const bool miss_over = __syncthreads_or(dm > kMissPart) != 0;  // these barriers also publish doff / goff
+  // (The reduction's barriers also publish doff / goff.)
+  const unsigned over = block_or_lds((ni > kGatherPart ? 1u : 0u) | (dm > kMissPart ? 2u : 0u) |
+                                         (dm > kSpecEntries ? 4u : 0u) | (ni > kSpecGather ? 8u : 0u),
+                                     L.scratch);
+  const bool gather_over = (over & 1u) != 0;
+  const bool miss_over = (over & 2u) != 0;
+  const bool direct = !gather_over && g <= kRankDirect;
+  // Entries past the ones read up front (all of them when active > kSpecChunks).
+  const bool rest = !spec || (over & 4u) != 0 || (direct && (over & 8u) != 0);
+  if (tid < active) L.cim[tid] = 0;  // (read above by this thread only)
 
   // 2. The handed-over definite misses, and the in-bin tokens for the ranking.
-  for (int f = tid; f < nd; f += kManageThreads) {
-    const int p = chunk_of(L.doff, active, f);
-    L.dmiss[f] = w.missl[(static_cast<int64_t>(b) * parts + p) * kMissPart + (f - L.doff[p])];
+  if (spec && sp < active) {
+    // Entries of chunk sp handed over: the offsets' differences.
+    const int dn = (sp + 1 < active ? L.doff[sp + 1] : nd) - L.doff[sp];
+    const int gn = (sp + 1 < active ? L.goff[sp + 1] : g) - L.goff[sp];
+    if (si < dn) L.dmiss[L.doff[sp] + si] = smiss[sp * kSpecEntries + si];
+    if (si + 32 < dn) L.dmiss[L.doff[sp] + si + 32] = smiss[sp * kSpecEntries + si + 32];
+    if (direct && si < gn && si < kSpecGather) {
+      const int f = L.goff[sp] + si;
+      const uint32_t* d = sgat + (sp * kSpecGather + si) * 3;
+      ltok[f] = static_cast<int>(d[0]);
+      lkey[f] = d[1];
+      lslot[f] = static_cast<int>(d[2]);
+    }
   }
-  const bool direct = !gather_over && g <= kRankDirect;
-  uint32_t* lkey = L.region;
-  int* ltok = reinterpret_cast<int*>(L.region + kRankDirect);
-  int my_t = 0;
-  uint32_t my_k = 0u;
-  int32_t my_slot = -1;
-  if (direct && tid < g) {
-    const int p = chunk_of(L.goff, active, tid);
-    const uint4 e = w.gather[(static_cast<int64_t>(b) * parts + p) * kGatherPart + (tid - L.goff[p])];
-    my_t = static_cast<int>(e.x);
-    my_k = e.y;
-    my_slot = static_cast<int32_t>(e.z);
-    ltok[tid] = my_t;
-    lkey[tid] = my_k;
+  if (rest) {
+    for (int f = tid; f < nd; f += kManageThreads) {
+      const int p = chunk_of(L.doff, active, f);
+      if (spec && f - L.doff[p] < kSpecEntries) continue;
+      L.dmiss[f] = w.missl[(static_cast<int64_t>(b) * parts + p) * kMissPart + (f - L.doff[p])];
+    }
+    if (direct) {
+      for (int f = tid; f < g; f += kManageThreads) {
+        const int p = chunk_of(L.goff, active, f);
+        if (spec && f - L.goff[p] < kSpecGather) continue;
+        const uint4 e = w.gather[(static_cast<int64_t>(b) * parts + p) * kGatherPart + (f - L.goff[p])];
+        ltok[f] = static_cast<int>(e.x);
+        lkey[f] = e.y;
+        lslot[f] = static_cast<int>(e.z);
+      }
+    }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. The threshold among the in-bin tokens (ties go to the lower token) and
   //    their classification: cached ones into the slot table, misses listed.
   uint32_t thr = 0u;
   int cutoff = INT_MAX;
-  auto classify = [&](int t, int32_t slot, bool selected, uint32_t key) {
+  auto classify = [&](int t, int32_t slot, bool selected, uint32_t key, bool patch) {
     if (slot >= 0 && slot < c) {
-      if (selected) {
-        stab[slot] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
-      } else {
-        stab[slot] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
-        skey[slot] = key;
+      const uint32_t ent = static_cast<uint32_t>(t) | ((selected ? kStateHit : kStateCand) << kStateShift);
+      stab[slot] = ent;
+      if (!selected) skey[slot] = key;
+      if (patch) {  // the victims' copy of the slot table
+        lst[slot] = ent;
+        lkv[slot] = key;
       }
     } else if (selected) {
       atomicAdd(&L.cim[t / kChunk], 1);
@@ -1176,18 +1265,29 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   if (direct) {
     // Rank pairwise: key descending, then token ascending.
     if (tid < g) {
+      const int my_t = ltok[tid];
+      const uint32_t my_k = lkey[tid];
+      const int32_t my_slot = lslot[tid];
       int rank = 0;
-      for (int j = 0; j < g; ++j) {
-        const uint32_t kj = lkey[j];
-        rank += (kj > my_k || (kj == my_k && ltok[j] < my_t)) ? 1 : 0;
+      // Four entries per LDS read (the lists hold kRankDirect entries; those
+      // past g are skipped).
+#pragma unroll 2
+      for (int j = 0; j < g; j += 4) {
+        const uint4 k4 = *reinterpret_cast<const uint4*>(lkey + j);
+        const int4 t4 = *reinterpret_cast<const int4*>(ltok + j);
+        const uint32_t kk[4] = {k4.x, k4.y, k4.z, k4.w};
+        const int tt4[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rank += (j + e < g && (kk[e] > my_k || (kk[e] == my_k && tt4[e] < my_t))) ? 1 : 0;
       }
       if (rank == k - 1) {  // the last selected token: the threshold and the tie cutoff
         L.bcast[0] = static_cast<int>(my_k);
         L.bcast[1] = my_t;
       }
-      classify(my_t, my_slot, rank < k, my_k);
+      classify(my_t, my_slot, rank < k, my_k, slots_in_regs);
     }
-    __syncthreads();
+    lds_barrier();  // the slot-table stores stay in flight
     thr = static_cast<uint32_t>(L.bcast[0]);
     cutoff = L.bcast[1];
   } else {
@@ -1231,32 +1331,45 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       load_bin(gi, key, inc);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (inc[e]) classify(4 * gi + e, pool[4 * gi + e], mtp0_selected(key[e], 4 * gi + e, thr, cutoff), key[e]);
+        if (inc[e]) classify(4 * gi + e, pool[4 * gi + e], mtp0_selected(key[e], 4 * gi + e, thr, cutoff), key[e], false);
     }
   }
-  __syncthreads();  // the slot table, cim and the in-bin miss list are complete
+  // The slot table, cim and the in-bin miss list are complete.  Only the
+  // global slot table's readers (the streamed paths) need the full barrier.
+  if (direct && slots_in_regs)
+    lds_barrier();
+  else
+    __syncthreads();
+  uint32_t st[kSlotRegs], kv[kSlotRegs];
+  if (slots_in_regs) {
+    if (direct) {
+#pragma unroll
+      for (int e = 0; e < kSlotRegs; ++e) {
+        st[e] = lst[tid * kSlotRegs + e];
+        kv[e] = lkv[tid * kSlotRegs + e];
+      }
+    } else {
+      load_slot_regs<kSlotRegs>(stab, skey, st, kv);  // after the streamed classification
+    }
+  }
 
   // 4. Misses per chunk, their bases, and the victims.
   const int mine = tid < active ? L.cdm[tid] + L.cim[tid] : 0;
   int m_all;
-  const int base = block_exclusive_scan(mine, L.scratch, &m_all);
+  const int base = block_exclusive_scan<true>(mine, L.scratch, &m_all);
   if (tid < active) L.goff[tid] = base;  // goff now holds the misses before each chunk
   const int m = min(m_all, kTopK);       // misses are selected tokens
   const int nib = *L.nibm;
   uint32_t* hist = L.region;
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  __syncthreads();
-  constexpr int kSlotRegs = 4;  // budgets up to kSlotRegs * kManageThreads slots keep their states in registers
-  const bool slots_in_regs = c <= kSlotRegs * kManageThreads;
-  uint32_t st[kSlotRegs], kv[kSlotRegs];
+  lds_barrier();
   int nv;
   if (slots_in_regs) {
-    load_slot_regs<kSlotRegs>(stab, skey, st, kv);
-    nv = select_victims_in_regs<kSlotRegs>(c, m, st, kv, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+    nv = select_victims_in_regs<kSlotRegs, true>(c, m, st, kv, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
   } else {
     nv = select_victims(c, m, stab, skey, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
   }
-  __syncthreads();  // the histogram is free again
+  lds_barrier();  // the histogram is free again
 
   // 5. The ordered miss list (ascending token): a chunk's definite misses and
   //    in-bin misses interleave by token; chunks follow one another.
@@ -1307,7 +1420,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       for (int e = 0; e < kItems; ++e)
         if (in[e] && mtp0_selected(u[e], t0 + e, thr, cutoff) && !(slot[e] >= 0 && slot[e] < c)) missm |= 1u << e;
       int tot;
-      int pos = L.goff[p] + block_exclusive_scan(__popc(missm), L.scratch, &tot);
+      int pos = L.goff[p] + block_exclusive_scan<true>(__popc(missm), L.scratch, &tot);
 #pragma unroll
       for (int e = 0; e < kItems; ++e)
         if ((missm >> e) & 1u) {
@@ -1316,7 +1429,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
         }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 6. Misses first (ascending token) paired with the ascending victim slots,
   //    and the pool update.
@@ -1343,7 +1456,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   for (int e = 0; e < kSlotRegs; ++e)
     if (i0 + e < c && (st[e] >> kStateShift) == kStateHit) hm |= 1u << e;
   int nhits;
-  const int below = block_exclusive_scan(__popc(hm), L.scratch, &nhits);  // hits in lower slots
+  const int below = block_exclusive_scan<true>(__popc(hm), L.scratch, &nhits);  // hits in lower slots
   int above = nhits - below - __popc(hm);                                  // hits in higher slots
 #pragma unroll
   for (int e = kSlotRegs - 1; e >= 0; --e)
@@ -1405,7 +1518,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a,
     for (int j = 0; j < 8; ++j) sum += cnt[j];
     if (tid == 0) bcast[0] = bcast[1] = 0;  // ordered before the writes below by the scan's barriers
     int total;
-    int acc = block_exclusive_scan(sum, scratch, &total);
+    int acc = block_exclusive_scan<true>(sum, scratch, &total);  // the token loads stay in flight
     if (acc < kTopK && kTopK <= acc + sum) {
 #pragma unroll
       for (int j = 7; j >= 0; --j) {
@@ -1416,7 +1529,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a,
         acc += cnt[j];
       }
     }
-    __syncthreads();
+    lds_barrier();
     bin = __builtin_amdgcn_readfirstlane(bcast[0]);
     above = __builtin_amdgcn_readfirstlane(bcast[1]);
   }
@@ -1447,7 +1560,9 @@ __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a,
   // One scan for both counts (each below 2^16): definite misses high, in-bin
   // tokens low; both hand-over slices keep token order.
   uint64_t tot;
-  const uint64_t pos = block_exclusive_scan4(static_cast<uint64_t>(__popc(missm)) << 16 | __popc(inbin), scratch64, &tot);
+  // (LDS-only barriers: the slot-table stores stay in flight until the arrival fence.)
+  const uint64_t pos =
+      block_exclusive_scan4<true>(static_cast<uint64_t>(__popc(missm)) << 16 | __popc(inbin), scratch64, &tot);
   int midx = static_cast<int>((pos >> 16) & 0xffffu);
   int iidx = static_cast<int>(pos & 0xffffu);
   int32_t* ml = w.missl + (static_cast<int64_t>(b) * parts + part) * kMissPart;

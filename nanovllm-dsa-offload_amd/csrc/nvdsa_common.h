@@ -113,9 +113,10 @@ __device__ inline void scan_barrier() {
 
 // Block-wide exclusive prefix sum of one int per thread (blockDim <= 1024,
 // multiple of 64).  `scratch` must hold blockDim/64 + 1 ints.  Returns the
-// exclusive prefix; *total receives the block sum.  Contains barriers: full
-// ones, or with LDS_ONLY barriers that order LDS only (for callers whose
-// global writes nobody reads before a later full barrier).
+// exclusive prefix; *total receives the block sum.  Every thread reads the
+// wave totals itself (independent LDS reads instead of one thread's chain).
+// Contains barriers: full ones, or with LDS_ONLY barriers that order LDS only
+// (for callers whose global writes nobody reads before a later full barrier).
 template <bool LDS_ONLY = false>
 __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
   const int lane = threadIdx.x & 63;
@@ -130,20 +131,18 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
   }
   if (lane == 63) scratch[wid] = x;
   scan_barrier<LDS_ONLY>();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int w = 0; w < nw; ++w) {
-      int t = scratch[w];
-      scratch[w] = run;
-      run += t;
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    if (w < nw) {
+      const int t = scratch[w];
+      before += w < wid ? t : 0;
+      tot += t;
     }
-    scratch[nw] = run;
   }
-  scan_barrier<LDS_ONLY>();
-  int excl = scratch[wid] + x - v;
-  *total = __builtin_amdgcn_readfirstlane(scratch[nw]);  // uniform: may steer barrier-containing code
-  scan_barrier<LDS_ONLY>();
-  return excl;
+  *total = __builtin_amdgcn_readfirstlane(tot);  // uniform: may steer barrier-containing code
+  scan_barrier<LDS_ONLY>();  // scratch is reused by the next scan
+  return before + x - v;
 }
 
 // Exclusive prefix of a 0/1 flag within the wave using a ballot.
