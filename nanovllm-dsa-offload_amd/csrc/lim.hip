@@ -961,7 +961,9 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
 //                 to the lower token), classifies them, selects the victims,
 //                 and writes the whole output row and the pool update.
 // The score kernel zeroes each request's histogram and finished-chunk counter.
-static_assert(kHistBins == 8 * kManageThreads, "lim_classify: eight first-digit bins per thread");
+constexpr int kHistPerThread = kHistBins / kManageThreads;  // lim_classify: first-digit bins per thread
+static_assert(kHistBins % kManageThreads == 0 && (kHistPerThread == 2 || kHistPerThread % 4 == 0),
+              "lim_classify: whole vector loads of first-digit bins per thread");
 static_assert(kChunk == 4096, "the gather list holds one chunk's worth of tokens");
 
 __device__ inline bool mtp0_selected(uint32_t key, int t, uint32_t thr, int cutoff) {
@@ -1504,26 +1506,39 @@ __global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a,
   bool in[kItems];
   load_tokens8(w.scores + static_cast<int64_t>(b) * cap, a.pool + static_cast<int64_t>(r) * cap, n, t0, u, slot, in);
   // The first-digit bin holding the 2048th largest key: thread tid owns bins
-  // [8 tb, 8 tb + 8), tb = 511 - tid, so ascending threads scan descending bins.
+  // [P tb, P tb + P), P = kHistPerThread, tb = 511 - tid, so ascending threads
+  // scan descending bins.
   int bin = 0, above = 0;
   {
+    constexpr int P = kHistPerThread;
     const int tb = kManageThreads - 1 - tid;
-    const uint32_t* gh = w.hist + static_cast<int64_t>(b) * kHistBins + 8 * tb;
-    const uint4 h0 = *reinterpret_cast<const uint4*>(gh);
-    const uint4 h1 = *reinterpret_cast<const uint4*>(gh + 4);
-    const int cnt[8] = {static_cast<int>(h0.x), static_cast<int>(h0.y), static_cast<int>(h0.z), static_cast<int>(h0.w),
-                        static_cast<int>(h1.x), static_cast<int>(h1.y), static_cast<int>(h1.z), static_cast<int>(h1.w)};
+    const uint32_t* gh = w.hist + static_cast<int64_t>(b) * kHistBins + P * tb;
+    int cnt[P];
+    if constexpr (P == 2) {
+      const uint2 h = *reinterpret_cast<const uint2*>(gh);
+      cnt[0] = static_cast<int>(h.x);
+      cnt[1] = static_cast<int>(h.y);
+    } else {
+#pragma unroll
+      for (int j = 0; j < P; j += 4) {
+        const uint4 h = *reinterpret_cast<const uint4*>(gh + j);
+        cnt[j] = static_cast<int>(h.x);
+        cnt[j + 1] = static_cast<int>(h.y);
+        cnt[j + 2] = static_cast<int>(h.z);
+        cnt[j + 3] = static_cast<int>(h.w);
+      }
+    }
     int sum = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sum += cnt[j];
+    for (int j = 0; j < P; ++j) sum += cnt[j];
     if (tid == 0) bcast[0] = bcast[1] = 0;  // ordered before the writes below by the scan's barriers
     int total;
     int acc = block_exclusive_scan<true>(sum, scratch, &total);  // the token loads stay in flight
     if (acc < kTopK && kTopK <= acc + sum) {
 #pragma unroll
-      for (int j = 7; j >= 0; --j) {
+      for (int j = P - 1; j >= 0; --j) {
         if (acc < kTopK && kTopK <= acc + cnt[j]) {
-          bcast[0] = 8 * tb + j;
+          bcast[0] = P * tb + j;
           bcast[1] = acc;
         }
         acc += cnt[j];
