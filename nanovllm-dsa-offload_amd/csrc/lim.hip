@@ -1342,36 +1342,83 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
     lds_barrier();
   else
     __syncthreads();
-  uint32_t st[kSlotRegs], kv[kSlotRegs];
+  // The slot states in registers (their keys only where victims are
+  // selected, below).
+  uint32_t st[kSlotRegs];
   if (slots_in_regs) {
-    if (direct) {
+    const uint32_t* src = direct ? lst : stab;  // (the global table after the streamed classification)
 #pragma unroll
-      for (int e = 0; e < kSlotRegs; ++e) {
-        st[e] = lst[tid * kSlotRegs + e];
-        kv[e] = lkv[tid * kSlotRegs + e];
-      }
-    } else {
-      load_slot_regs<kSlotRegs>(stab, skey, st, kv);  // after the streamed classification
+    for (int j = 0; j < kSlotRegs; j += 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(src + tid * kSlotRegs + j);
+      st[j] = v.x;
+      st[j + 1] = v.y;
+      st[j + 2] = v.z;
+      st[j + 3] = v.w;
     }
   }
 
-  // 4. Misses per chunk, their bases, and the victims.
+  // 4. Misses per chunk, their bases, and the victims.  With the slots in
+  //    registers one scan counts the misses before each chunk, the non-hit
+  //    slots (victim candidates) and the hit slots before each thread's; when
+  //    every non-hit slot is a victim (C = 2048 with a full pool) the victims
+  //    come straight from it, in ascending slot order.
   const int mine = tid < active ? L.cdm[tid] + L.cim[tid] : 0;
-  int m_all;
-  const int base = block_exclusive_scan<true>(mine, L.scratch, &m_all);
+  const int i0 = tid * kSlotRegs;
+  unsigned nh = 0u, hm = 0u;  // this thread's non-hit and hit slots below c
+  if (slots_in_regs) {
+#pragma unroll
+    for (int e = 0; e < kSlotRegs; ++e)
+      if (i0 + e < c) {
+        if ((st[e] >> kStateShift) == kStateHit)
+          hm |= 1u << e;
+        else
+          nh |= 1u << e;
+      }
+  }
+  // Fields: misses [42, 64), non-hit slots [21, 42), hits [0, 21) (block
+  // totals stay below 2^21: at most 512 chunks of 4096 tokens, c < 2^14).
+  uint64_t tot4;
+  const uint64_t ex4 = block_exclusive_scan4<true>(static_cast<uint64_t>(mine) << 42 |
+                                                       static_cast<uint64_t>(__popc(nh)) << 21 | __popc(hm),
+                                                   L.scratch64, &tot4);
+  constexpr uint64_t kField = (uint64_t{1} << 21) - 1;
+  const int base = static_cast<int>(ex4 >> 42);
+  const int m_all = static_cast<int>(tot4 >> 42);
+  const int nonhit = static_cast<int>((tot4 >> 21) & kField);
+  const int nhits = static_cast<int>(tot4 & kField);
   if (tid < active) L.goff[tid] = base;  // goff now holds the misses before each chunk
+  L.cim[tid] = static_cast<int>(ex4 & kField);  // hits in lower slots, for step 7 (cim is free now)
   const int m = min(m_all, kTopK);       // misses are selected tokens
   const int nib = *L.nibm;
-  uint32_t* hist = L.region;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  lds_barrier();
   int nv;
-  if (slots_in_regs) {
-    nv = select_victims_in_regs<kSlotRegs, true>(c, m, st, kv, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+  if (slots_in_regs && m >= nonhit) {
+    int pos = static_cast<int>((ex4 >> 21) & kField);
+#pragma unroll
+    for (int e = 0; e < kSlotRegs; ++e)
+      if ((nh >> e) & 1u) {
+        L.vsl[pos] = i0 + e;
+        L.vev[pos] = (st[e] >> kStateShift) == kStateCand ? static_cast<int>(st[e] & kTokenMask) : -1;
+        ++pos;
+      }
+    nv = nonhit;
   } else {
-    nv = select_victims(c, m, stab, skey, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+    uint32_t kv[kSlotRegs];
+    if (slots_in_regs) {
+      const uint32_t* src = direct ? lkv : skey;
+#pragma unroll
+      for (int e = 0; e < kSlotRegs; ++e) kv[e] = src[tid * kSlotRegs + e];
+    }
+    lds_barrier();  // lkv is read before the histogram overwrites it
+    uint32_t* hist = L.region;
+    for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+    lds_barrier();
+    if (slots_in_regs) {
+      nv = select_victims_in_regs<kSlotRegs, true>(c, m, st, kv, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+    } else {
+      nv = select_victims(c, m, stab, skey, L.vsl, hist, L.scratch, L.bcast, L.red, L.vev);
+    }
   }
-  lds_barrier();  // the histogram is free again
+  lds_barrier();  // the victims and goff are published; the histogram is free again
 
   // 5. The ordered miss list (ascending token): a chunk's definite misses and
   //    in-bin misses interleave by token; chunks follow one another.
@@ -1452,17 +1499,15 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
     write_hit_rows(a, b, c, m, stab, L.scratch);
     return;
   }
-  const int i0 = tid * kSlotRegs;
-  unsigned hm = 0u;
+  unsigned hm7 = 0u;
 #pragma unroll
   for (int e = 0; e < kSlotRegs; ++e)
-    if (i0 + e < c && (st[e] >> kStateShift) == kStateHit) hm |= 1u << e;
-  int nhits;
-  const int below = block_exclusive_scan<true>(__popc(hm), L.scratch, &nhits);  // hits in lower slots
-  int above = nhits - below - __popc(hm);                                  // hits in higher slots
+    if (i0 + e < c && (st[e] >> kStateShift) == kStateHit) hm7 |= 1u << e;
+  const int below = L.cim[tid];                 // hits in lower slots (this thread's own word)
+  int above = nhits - below - __popc(hm7);      // hits in higher slots
 #pragma unroll
   for (int e = kSlotRegs - 1; e >= 0; --e)
-    if ((hm >> e) & 1u) {
+    if ((hm7 >> e) & 1u) {
       const int pos = m + above;
       if (pos < kTopK) {
         out_src[pos] = static_cast<int32_t>(st[e] & kTokenMask);
@@ -1478,7 +1523,9 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   if (tid == 0) a.miss_counts[b] = m;
 }
 
-__global__ __launch_bounds__(kManageThreads) void lim_classify_kernel(LimArgs a, LimWs w, int parts) {
+// At most 128 VGPRs (four waves per SIMD): two workgroups per CU, as the ~74 KB of
+// LDS allows, for launches of more chunks than CUs.
+__global__ __launch_bounds__(kManageThreads, 4) void lim_classify_kernel(LimArgs a, LimWs w, int parts) {
   __shared__ uint32_t region[kBins];
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
