@@ -730,6 +730,17 @@ __device__ __forceinline__ void load_slot_regs(const uint32_t* stab, const uint3
   }
 }
 
+template <int ITEMS>
+__device__ __forceinline__ void load_slot_states(const uint32_t* stab, uint32_t (&st)[ITEMS]) {
+  static_assert(ITEMS % 4 == 0, "vector loads of four slots");
+  const int i0 = threadIdx.x * ITEMS;
+#pragma unroll
+  for (int j = 0; j < ITEMS / 4; ++j) {
+    const uint4 a = *reinterpret_cast<const uint4*>(stab + i0 + 4 * j);
+    st[4 * j] = a.x; st[4 * j + 1] = a.y; st[4 * j + 2] = a.z; st[4 * j + 3] = a.w;
+  }
+}
+
 // select_victims with the slot states and keys held in registers (from
 // load_slot_regs): thread t owns slots [t*ITEMS, (t+1)*ITEMS) (slot order =
 // thread-major order).  Same result as select_victims; requires
@@ -1139,6 +1150,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   //    across the scans.
   constexpr int kSlotRegs = 4;  // budgets up to kSlotRegs * kManageThreads slots keep their states in registers
   const bool slots_in_regs = c <= kSlotRegs * kManageThreads;
+  const bool keyed = c > kTopK;  // victims are chosen by key; at c = kTopK every non-hit slot is one
   const bool spec = active <= kSpecChunks;
   const int sp = tid >> 5, si = tid & 31;
   uint32_t* lkey = L.region;
@@ -1165,7 +1177,12 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       if (si < kSpecGather) sg = w.gather[(static_cast<int64_t>(b) * parts + sp) * kGatherPart + si];
     }
     uint32_t st[kSlotRegs], kv[kSlotRegs];
-    if (slots_in_regs) load_slot_regs<kSlotRegs>(stab, skey, st, kv);
+    if (slots_in_regs) {
+      if (keyed)
+        load_slot_regs<kSlotRegs>(stab, skey, st, kv);
+      else
+        load_slot_states<kSlotRegs>(stab, st);
+    }
     if (tid < active) {
       L.cdm[tid] = dm;
       L.cim[tid] = ni;  // in-bin count for now; the in-bin miss count below
@@ -1184,7 +1201,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
 #pragma unroll
       for (int e = 0; e < kSlotRegs; ++e) {
         lst[tid * kSlotRegs + e] = st[e];
-        lkv[tid * kSlotRegs + e] = kv[e];
+        if (keyed) lkv[tid * kSlotRegs + e] = kv[e];
       }
     }
   }
@@ -1254,10 +1271,10 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
     if (slot >= 0 && slot < c) {
       const uint32_t ent = static_cast<uint32_t>(t) | ((selected ? kStateHit : kStateCand) << kStateShift);
       stab[slot] = ent;
-      if (!selected) skey[slot] = key;
+      if (!selected && keyed) skey[slot] = key;
       if (patch) {  // the victims' copy of the slot table
         lst[slot] = ent;
-        lkv[slot] = key;
+        if (keyed) lkv[slot] = key;
       }
     } else if (selected) {
       atomicAdd(&L.cim[t / kChunk], 1);
@@ -1404,9 +1421,18 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   } else {
     uint32_t kv[kSlotRegs];
     if (slots_in_regs) {
-      const uint32_t* src = direct ? lkv : skey;
+      if (keyed) {
+        const uint32_t* src = direct ? lkv : skey;
 #pragma unroll
-      for (int e = 0; e < kSlotRegs; ++e) kv[e] = src[tid * kSlotRegs + e];
+        for (int e = 0; e < kSlotRegs; ++e) kv[e] = src[tid * kSlotRegs + e];
+      } else {
+        // c = kTopK with more non-hit slots than misses (a pool naming one
+        // slot twice): no key table was kept, a candidate slot's key is its
+        // token's score.
+#pragma unroll
+        for (int e = 0; e < kSlotRegs; ++e)
+          kv[e] = (st[e] >> kStateShift) == kStateCand ? score_key(s[st[e] & kTokenMask]) : 0u;
+      }
     }
     lds_barrier();  // lkv is read before the histogram overwrites it
     uint32_t* hist = L.region;
@@ -1613,7 +1639,7 @@ __global__ __launch_bounds__(kManageThreads, 4) void lim_classify_kernel(LimArgs
         stab[slot[e]] = static_cast<uint32_t>(t) | (kStateHit << kStateShift);
       } else {
         stab[slot[e]] = static_cast<uint32_t>(t) | (kStateCand << kStateShift);
-        skey[slot[e]] = u[e];
+        if (c > kTopK) skey[slot[e]] = u[e];  // (at c = kTopK every non-hit slot is a victim)
       }
     } else if (selected) {
       missm |= 1u << e;
