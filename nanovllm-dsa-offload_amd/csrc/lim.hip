@@ -1446,9 +1446,23 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   }
   lds_barrier();  // the victims and goff are published; the histogram is free again
 
-  // 5. The ordered miss list (ascending token): a chunk's definite misses and
-  //    in-bin misses interleave by token; chunks follow one another.
-  int* misstok = reinterpret_cast<int*>(L.region);
+  // 5. The misses in ascending token order -- a chunk's definite misses and
+  //    in-bin misses interleave by token, chunks follow one another -- each
+  //    written where its position lands, paired with the ascending victim
+  //    slots, with the pool update.  (Pool writes here touch only misses'
+  //    entries and evicted tokens', which are unselected, so the ordered pass
+  //    below still classifies its chunk's tokens correctly.)
+  auto emit = [&](int pos, int t) {
+    if (pos >= m) return;
+    const int d = pos < nv ? L.vsl[pos] : -1;
+    const int evicted = pos < nv ? L.vev[pos] : -1;  // an unselected token, or -1 for a free slot
+    out_src[pos] = t;
+    out_dst[pos] = d;
+    if (d >= 0) {
+      if (evicted >= 0) pool[evicted] = -1;
+      pool[t] = d;
+    }
+  };
   for (int f = tid; f < nd; f += kManageThreads) {
     const int p = chunk_of(L.doff, active, f);
     if (L.cdm[p] > kMissPart) continue;  // placed by the ordered pass below
@@ -1458,8 +1472,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       const int x = L.ibm[j];
       before_ib += (x < t && x >= p * kChunk) ? 1 : 0;
     }
-    const int pos = L.goff[p] + (f - L.doff[p]) + before_ib;
-    if (pos < kTopK) misstok[pos] = t;
+    emit(L.goff[p] + (f - L.doff[p]) + before_ib, t);
   }
   for (int j = tid; j < nib; j += kManageThreads) {
     const int t = L.ibm[j];
@@ -1477,12 +1490,12 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       const int x = L.ibm[j2];
       before_ib += (x < t && x >= p * kChunk) ? 1 : 0;
     }
-    const int pos = L.goff[p] + (lo_i - L.doff[p]) + before_ib;
-    if (pos < kTopK) misstok[pos] = t;
+    emit(L.goff[p] + (lo_i - L.doff[p]) + before_ib, t);
   }
   if (miss_over) {
     // Chunks with more definite misses than their slice: one ordered pass
-    // over the chunk's tokens (the pool is not updated yet).
+    // over the chunk's tokens (every thread reads its tokens' pool entries
+    // before the scan's barriers, ahead of any write of this pass).
     for (int p = 0; p < active; ++p) {
       if (L.cdm[p] <= kMissPart) continue;  // uniform
       const int t0 = p * kChunk + tid * kItems;
@@ -1499,24 +1512,9 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
 #pragma unroll
       for (int e = 0; e < kItems; ++e)
         if ((missm >> e) & 1u) {
-          if (pos < kTopK) misstok[pos] = t0 + e;
+          emit(pos, t0 + e);
           ++pos;
         }
-    }
-  }
-  lds_barrier();
-
-  // 6. Misses first (ascending token) paired with the ascending victim slots,
-  //    and the pool update.
-  for (int pos = tid; pos < m; pos += kManageThreads) {
-    const int t = misstok[pos];
-    const int d = pos < nv ? L.vsl[pos] : -1;
-    const int evicted = pos < nv ? L.vev[pos] : -1;  // an unselected token, or -1 for a free slot
-    out_src[pos] = t;
-    out_dst[pos] = d;
-    if (d >= 0) {
-      if (evicted >= 0) pool[evicted] = -1;
-      pool[t] = d;
     }
   }
 
