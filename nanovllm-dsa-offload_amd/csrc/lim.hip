@@ -1102,7 +1102,7 @@ struct ResolveLds {
   uint32_t* red;
   int* bcast;
   int* cdm;    // [active] definite misses of each chunk
-  int* cim;    // [active] in-bin misses of each chunk
+  int* cim;    // [active] in-bin misses of each chunk; from step 4 each thread's hit slots below its own
   int* doff;   // [active] offset of each chunk's definite misses in dmiss
   int* goff;   // [active] offset of each chunk's in-bin tokens, then the misses before each chunk
   int* dmiss;  // [kTopK] definite misses, chunk by chunk (each in token order)
