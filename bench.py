@@ -87,7 +87,7 @@ def parse_args():
 
 # ---- hardware-counter helpers ------------------------------------------------
 # The MTP0 management kernels, in launch order (one workgroup per 4096-token chunk).
-MANAGE_KERNELS = ("lim_hist_kernel", "lim_classify_kernel")
+MANAGE_KERNELS = ("lim_hist_kernel", "lim_classify_kernel", "lim_chunks_kernel", "lim_resolve_kernel")
 PMC_KERNELS = ("lim_score_kernel", "lim_mtp_pass_a_kernel", "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
                "lim_threshold_kernel") + MANAGE_KERNELS + ("sfa_split_kernel",
                "sfa_combine_kernel", "scatter_copy_kernel", "indexer_project_kernel")
@@ -272,8 +272,16 @@ class Chain:
         return e0.elapsed_time(e1) / steps
 
 
+def _ran(kt, names):
+    """The kernels of ``names`` that ran inside the timer (MTP0 management runs
+    lim_classify_kernel, or lim_chunks_kernel + lim_resolve_kernel for launches
+    of more than 512 chunks)."""
+    seen = {k for k, _ in kt.records}
+    return tuple(n for n in names if n in seen)
+
+
 def _kernel_table(kt, names):
-    return {n: round(kt.mean_ms(n) * 1000, 2) for n in names}
+    return {n: round(kt.mean_ms(n) * 1000, 2) for n in _ran(kt, names)}
 
 
 def measure_cfg0(torch, np, dev, seed: int, steps: int = 20):
@@ -530,9 +538,10 @@ def main() -> int:
     torch.cuda.synchronize()
     del narrow_graphs, narrow, tn
 
-    k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel",) + MANAGE_KERNELS +
+    manage_ran = _ran(kt_fuse, MANAGE_KERNELS)
+    k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel",) + manage_ran +
          ("sfa_split_kernel_fused", "sfa_combine_kernel")}
-    k["lim_manage"] = sum(k[name] for name in MANAGE_KERNELS)
+    k["lim_manage"] = sum(k[name] for name in manage_ran)
     ks = {name: kt_split.mean_ms(name) for name in ("scatter_copy_kernel", "sfa_split_kernel")}
 
     # ---- roofline of the index-key scan (lim_score_kernel) ------------------
@@ -610,11 +619,11 @@ def main() -> int:
             "fuse_graph_step": round(value_us, 2), "fuse_graph_1step": round(graph1_ms * 1000, 2),
             "fuse_eager_step": round(eager_ms * 1000, 2),
             "fuse_graph_step_narrow_tables": round(narrow_ms * 1000, 2),
-            "lim_manage_narrow_tables": round(sum(kt_narrow.mean_ms(n) for n in MANAGE_KERNELS) * 1000, 2),
+            "lim_manage_narrow_tables": round(sum(kt_narrow.mean_ms(n) for n in _ran(kt_narrow, MANAGE_KERNELS)) * 1000, 2),
             "split_graph_step": round(split_graph_ms * 1000, 2),
             "split_eager_step": round(split_ms * 1000, 2),
             "lim_score": round(k["lim_score_kernel"] * 1000, 2), "lim_manage": round(k["lim_manage"] * 1000, 2),
-            **{name[:-len("_kernel")]: round(k[name] * 1000, 2) for name in MANAGE_KERNELS},
+            **{name[:-len("_kernel")]: round(k[name] * 1000, 2) for name in manage_ran},
             "fused_copy_sfa_split": round(k["sfa_split_kernel_fused"] * 1000, 2),
             "sfa_combine": round(k["sfa_combine_kernel"] * 1000, 2),
             "scatter_copy": round(ks["scatter_copy_kernel"] * 1000, 2), "sfa_split": round(ks["sfa_split_kernel"] * 1000, 2),
@@ -631,7 +640,7 @@ def main() -> int:
 
 
 def _kernel_means(kt, names):
-    return {n: round(kt.mean_ms(n) * 1000, 2) for n in names}
+    return _kernel_table(kt, names)
 
 
 def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):

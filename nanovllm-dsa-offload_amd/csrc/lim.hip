@@ -56,6 +56,10 @@ constexpr int kMissPart = 256;                    // MTP0: definite misses a chu
 constexpr int kSpecChunks = 16;                   // MTP0 last chunk: requests of up to this many chunks ...
 constexpr int kSpecEntries = 64;                  // ... read this many definite misses per chunk up front
 constexpr int kSpecGather = 16;                   // ... and this many in-bin tokens
+// MTP0: launches of up to this many chunks (two 512-thread workgroups per CU on
+// 256 CUs) resolve each request in its last chunk; larger ones (bs=64 at 64K:
+// 1024) classify in a light kernel and resolve in a second one.
+constexpr int64_t kResidentChunks = 512;
 constexpr int kSlotStride = kMaxCacheTokens + 1;  // 16384 entries per request
 constexpr int kTableStride = kSlotStride + kManageThreads;  // workspace slot tables: + one junk word per thread
 constexpr uint32_t kStateShift = 24;
@@ -78,7 +82,7 @@ struct LimWs {
   int32_t* done;        // MTP0: [B] chunks that finished lim_classify_kernel
   uint2* ranges;        // MTP0: [B, S_cap/128] smallest and largest score key of each 128-token block
   uint32_t* hist;       // MTP0: [B, kHistBins] first-digit histogram of the request's keys
-  uint32_t* rowsel;     // MTP0: [B, 4] the request's smallest key and first-digit shift
+  uint32_t* rowsel;     // MTP0: [B, 4] the request's smallest key, first-digit shift; the bin and the count above it (lim_chunks_kernel)
   uint4* gather;        // MTP0: [B, parts, kGatherPart] each chunk's (token, key, pool slot, -) in the threshold's first-digit bin
   int32_t* missl;       // MTP0: [B, parts, kMissPart] each chunk's definite misses (selected, not cached), in token order
 };
@@ -1547,29 +1551,21 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
   if (tid == 0) a.miss_counts[b] = m;
 }
 
-// At most 128 VGPRs (four waves per SIMD): two workgroups per CU, as the ~74 KB of
-// LDS allows, for launches of more chunks than CUs.
-__global__ __launch_bounds__(kManageThreads, 4) void lim_classify_kernel(LimArgs a, LimWs w, int parts) {
-  __shared__ uint32_t region[kBins];
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
-  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
-  __shared__ int bcast[4];
-  __shared__ int cdm[kManageThreads], cim[kManageThreads], doff[kManageThreads], goff[kManageThreads];
-  __shared__ int dmiss[kTopK], ibm[kTopK], vsl[kTopK], vev[kTopK];
-  __shared__ int nibm;
-  __shared__ int last;
-  const int b = blockIdx.x / parts;
-  const int part = blockIdx.x - b * parts;
+// One 4096-token chunk of an MTP0 request (every launch shape): the row's
+// first-digit bin holding the 2048th largest key (from the request's
+// histogram) and the count above it; the chunk's cached tokens go to the slot
+// table, its definite misses and in-bin tokens to its hand-over slices, its
+// counts to part_counts.  The stores stay in flight (LDS-only barriers).
+struct ChunkSel {
+  uint32_t bin;
+  int above;
+};
+
+__device__ __forceinline__ ChunkSel classify_chunk(const LimArgs& a, const LimWs& w, int parts, int b, int part, int n,
+                                                   int c, int r, uint32_t lo, int shift, int* scratch,
+                                                   uint64_t* scratch64, int* bcast) {
   const int tid = threadIdx.x;
-  const int n = a.num_candidates[b];
-  const int c = a.num_cache[b];
-  const int r = a.pool_entries[b];
-  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || part * kChunk >= n) return;
-  const int active = static_cast<int>(ceil_div(n, kChunk));  // chunks that arrive below
   const int64_t cap = a.source_capacity;
-  const uint32_t lo = w.rowsel[4 * b];
-  const int shift = static_cast<int>(w.rowsel[4 * b + 1]);
   // This chunk's tokens: the loads are in flight during the bin search.
   const int t0 = part * kChunk + tid * kItems;
   uint32_t u[kItems];
@@ -1669,6 +1665,33 @@ __global__ __launch_bounds__(kManageThreads, 4) void lim_classify_kernel(LimArgs
     counts[0] = static_cast<int>((tot >> 16) & 0xffffu);
     counts[1] = static_cast<int>(tot & 0xffffu);
   }
+  return ChunkSel{static_cast<uint32_t>(bin), above};
+}
+
+// At most 128 VGPRs (four waves per SIMD): two workgroups per CU, as the ~74 KB of
+// LDS allows.  Used while every chunk of the launch is resident at once
+// (kResidentChunks); larger launches take lim_chunks_kernel + lim_resolve_kernel.
+__global__ __launch_bounds__(kManageThreads, 4) void lim_classify_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ uint32_t region[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  __shared__ int cdm[kManageThreads], cim[kManageThreads], doff[kManageThreads], goff[kManageThreads];
+  __shared__ int dmiss[kTopK], ibm[kTopK], vsl[kTopK], vev[kTopK];
+  __shared__ int nibm;
+  __shared__ int last;
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
+  const int tid = threadIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || part * kChunk >= n) return;
+  const int active = static_cast<int>(ceil_div(n, kChunk));  // chunks that arrive below
+  const uint32_t lo = w.rowsel[4 * b];
+  const int shift = static_cast<int>(w.rowsel[4 * b + 1]);
+  const ChunkSel sel = classify_chunk(a, w, parts, b, part, n, c, r, lo, shift, scratch, scratch64, bcast);
   // The barrier waits for every wave's stores; one release fence then makes
   // them visible device-wide before the arrival count, and the last chunk of
   // the request to arrive acquires the others' (one agent-scope fence each
@@ -1683,7 +1706,49 @@ __global__ __launch_bounds__(kManageThreads, 4) void lim_classify_kernel(LimArgs
   __syncthreads();
   if (!last) return;
   const ResolveLds L{region, scratch, scratch64, red, bcast, cdm, cim, doff, goff, dmiss, ibm, &nibm, vsl, vev};
-  mtp0_resolve(a, w, b, n, c, r, parts, active, static_cast<uint32_t>(bin), kTopK - above, lo, shift, L);
+  mtp0_resolve(a, w, b, n, c, r, parts, active, sel.bin, kTopK - sel.above, lo, shift, L);
+}
+
+// Launches of more chunks than stay resident next to the last chunk's LDS:
+// the chunks alone (a small footprint, so all of them are resident), then
+// lim_resolve_kernel, one workgroup per request.  Chunk 0 of a request leaves
+// the bin and the count above it in rowsel (every chunk finds the same).
+__global__ __launch_bounds__(kManageThreads) void lim_chunks_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
+  __shared__ int bcast[4];
+  const int b = blockIdx.x / parts;
+  const int part = blockIdx.x - b * parts;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows) || part * kChunk >= n) return;
+  const ChunkSel sel = classify_chunk(a, w, parts, b, part, n, c, r, w.rowsel[4 * b],
+                                      static_cast<int>(w.rowsel[4 * b + 1]), scratch, scratch64, bcast);
+  if (part == 0 && threadIdx.x == 0) {
+    w.rowsel[4 * b + 2] = sel.bin;
+    w.rowsel[4 * b + 3] = static_cast<uint32_t>(sel.above);
+  }
+}
+
+__global__ __launch_bounds__(kManageThreads, 4) void lim_resolve_kernel(LimArgs a, LimWs w, int parts) {
+  __shared__ uint32_t region[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint64_t scratch64[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  __shared__ int cdm[kManageThreads], cim[kManageThreads], doff[kManageThreads], goff[kManageThreads];
+  __shared__ int dmiss[kTopK], ibm[kTopK], vsl[kTopK], vev[kTopK];
+  __shared__ int nibm;
+  const int b = blockIdx.x;
+  const int n = a.num_candidates[b];
+  const int c = a.num_cache[b];
+  const int r = a.pool_entries[b];
+  if (!lim_row_valid(n, c, r, a.source_capacity, a.pool_rows)) return;
+  const uint32_t* sel = w.rowsel + 4 * b;
+  const ResolveLds L{region, scratch, scratch64, red, bcast, cdm, cim, doff, goff, dmiss, ibm, &nibm, vsl, vev};
+  mtp0_resolve(a, w, b, n, c, r, parts, static_cast<int>(ceil_div(n, kChunk)), sel[2], kTopK - static_cast<int>(sel[3]),
+               sel[0], static_cast<int>(sel[1]), L);
 }
 
 // ---------------------------------------------------------------------------
@@ -2128,7 +2193,12 @@ hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   const dim3 pgrid(static_cast<uint32_t>(a.batch * parts));
   if (Q == 1) {
     launch_kernel(kKernLimHist, lim_hist_kernel, pgrid, mblock, stream, a, w, parts);
-    launch_kernel(kKernLimClassify, lim_classify_kernel, pgrid, mblock, stream, a, w, parts);
+    if (a.batch * parts <= kResidentChunks) {
+      launch_kernel(kKernLimClassify, lim_classify_kernel, pgrid, mblock, stream, a, w, parts);
+    } else {
+      launch_kernel(kKernLimChunks, lim_chunks_kernel, pgrid, mblock, stream, a, w, parts);
+      launch_kernel(kKernLimResolve, lim_resolve_kernel, mgrid, mblock, stream, a, w, parts);
+    }
     return hipGetLastError();
   }
   // MTP3: thresholds first, one workgroup per (request, query) score row.

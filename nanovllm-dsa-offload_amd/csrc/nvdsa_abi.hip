@@ -183,7 +183,9 @@ const char* nvdsa_kernel_name(int32_t kernel_id) {
                                 "sfa_combine_kernel",    "lidu_init_kernel", "lidu_shared_kernel",
                                 "lim_threshold_kernel",  "lim_mtp_victims_kernel", "lim_mtp_pass_b_kernel",
                                 "sfa_mtp_overlap_kernel", "sfa_split_kernel_copied", "indexer_project_kernel",
-                                "indexer_rope_kernel", "persist_blocks_kernel", "lim_classify_kernel"};
+                                "indexer_rope_kernel", "persist_blocks_kernel", "lim_classify_kernel",
+                                "lim_chunks_kernel",   "lim_resolve_kernel"};
+  static_assert(sizeof(names) / sizeof(names[0]) == nvdsa::kKernCount, "one name per kernel id");
   if (kernel_id < 0 || kernel_id >= nvdsa::kKernCount) return "unknown";
   return names[kernel_id];
 }

@@ -31,7 +31,9 @@ enum KernelId : int {
   kKernIdxRope = 15,
   kKernPersist = 16,
   kKernLimClassify = 17,
-  kKernCount = 18
+  kKernLimChunks = 18,
+  kKernLimResolve = 19,
+  kKernCount = 20
 };
 // Timing events for the next launch of `kernel_id` when instrumentation is
 // on for the calling thread (nvdsa_profile_begin); both null otherwise.

@@ -152,6 +152,43 @@ def test_lim_cold_pool_rows_bit_exact(n_tokens, cache_tokens):
     assert (ints(d["miss_counts"]) == 0).all()
 
 
+def test_lim_large_launch_bit_exact():
+    """More chunk workgroups than stay resident beside the last chunk's LDS:
+    40 requests on the model runner's 65536-wide tables are 640 chunks, so the
+    selection classifies in lim_chunks_kernel and resolves each request in
+    lim_resolve_kernel.  Warm and cold pool rows, 4096-16384 tokens, C from
+    2048 to 6144: every output and the pool bit-exact (columns past the
+    requests untouched), and the repeat call has no misses."""
+    from _chain import check_lim, run_lim, widen_layout
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import make_chain_case
+
+    rng = np.random.default_rng(53)
+    B = 40
+    lens = [int(x) for x in rng.choice([4096, 6144, 9216, 12288, 16384], size=B)]
+    caches = [min(int(x), n) for x, n in zip(rng.choice([2048, 3072, 6144], size=B), lens)]
+    case = make_chain_case(B, lens, caches, [int(x) for x in rng.integers(1, 128, size=B)], seed=53)
+    t = case.tensors
+    for row in ints(t["req_pool_entries"])[:3]:
+        t["cache_slots_pool"][int(row)].fill_(-1)
+    print("LIM large launch: 40 requests on 65536-wide tables", flush=True)
+    expect = oracle_lim(case)
+    assert (expect["miss_counts"][:3] == 2048).all()
+    d = case.to_device("cuda", host_mapped=False)
+    cap0 = d.tensors["cache_slots_pool"].shape[1]
+    w = widen_layout(d.tensors, 65536, pad=0)
+    wide_init = ints(w["cache_slots_pool"])
+    with _lib.KernelTimer(capacity=64) as kt:
+        run_lim(w, False)
+        torch.cuda.synchronize()
+    names = {k for k, _ in kt.records}
+    assert {"lim_chunks_kernel", "lim_resolve_kernel"} <= names and "lim_classify_kernel" not in names, names
+    check_lim(w, expect, False, "large launch", pool_cols=cap0)
+    assert np.array_equal(ints(w["cache_slots_pool"])[:, cap0:], wide_init[:, cap0:])
+    run_lim(w, False)
+    assert (ints(w["miss_counts"]) == 0).all()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("heads", [32, 64])
 def test_lim_random_bit_exact(dtype, heads):
