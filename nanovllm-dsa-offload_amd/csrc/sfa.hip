@@ -11,13 +11,18 @@
 //   o = softmax(scale * (q . ckv + q_rope . kpe)) . ckv     fp32 accumulate, 16-bit store.
 //
 // Kernel design (split-KV flash decode):
-//   grid = rows x splits x ceil(heads/64); a 256-thread workgroup owns one
-//   row, one split of its key list and 64 heads (16 heads per wavefront).
-//   Keys are processed in tiles of 32.  Each lane keeps its query operand
-//   (one head, 18 x 16 bytes of the 576 dims) in registers for the whole
-//   split; each tile is gathered row-contiguous into LDS (conflict-free
-//   16-byte operand reads for S; the V^T operand of the PV product comes
-//   from transposing ds_read_b64_tr_b16 reads).  S^T = K . Q^T and
+//   grid = rows x splits x ceil(heads/64); a 512-thread workgroup owns one
+//   row, one split of its key list and 64 heads.  Its 8 wavefronts are 4
+//   pairs, one pair per 16 heads; the two waves of a pair (two per SIMD,
+//   so one hides the other's LDS and MFMA latency) split the work by
+//   dimension: wave half d takes S's dims [288d, 288d + 288) and the
+//   output's latent dims [256d, 256d + 256).  Keys are processed in tiles
+//   of 32.  Each lane keeps its query operand (one head, 9 x 16 bytes of
+//   its 288 dims) in registers for the whole split; each tile is gathered
+//   row-contiguous into LDS (conflict-free 16-byte operand reads for S; the
+//   V^T operand of the PV product comes from transposing ds_read_b64_tr_b16
+//   reads).  The pair adds its two partial S tiles through LDS, so both
+//   waves hold the same S and run the same softmax.  S^T = K . Q^T and
 //   O^T = V^T . P^T run on v_mfma_f32_16x16x32; the online softmax is in
 //   base 2 with a running max that moves only when exceeded by more than
 //   kMaxSlack (few numerator rescales), and P enters the PV product as a
@@ -44,12 +49,15 @@ namespace nvdsa {
 namespace {
 
 constexpr int kTileKeys = 32;
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 512;
+constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kHeadsPerBlock = 64;
-constexpr int kKStride = kQkDim + 8;       // LDS row of the key tile (elements)
-constexpr int kQStride = kQkDim + 8;       // LDS row of the staged queries
+constexpr int kKStride = kQkDim + 16;      // LDS row of the key tile (elements; 1184 B, fewest bank conflicts)
 constexpr int kChunksPerKey = kQkDim * 2 / 16;  // 72 x 16 bytes
-constexpr int kChunksPerThread = kTileKeys * kChunksPerKey / kAttnThreads;  // 9
+// Tile loads per thread: 2304 16-byte chunks over 512 threads (4.5 each).
+constexpr int kChunksPerThread = 5;
+constexpr int kSChunks = kQkDim / 32 / 2;  // 9 MFMA k-steps of 32 dims: one wave's half of S
+constexpr int kVDims = kCkvDim / 2;        // 256 latent dims of the output per wave
 constexpr int kMaxSplits = 64;
 constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per window (one key per thread)
 constexpr int kWindowKeys = kWindowTiles * kTileKeys;
@@ -152,9 +160,11 @@ enum KeyMode : int {
 template <typename T, bool FUSED, int MODE>
 __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials& part, int splits, int split_base,
                                                int splits_total, int64_t bid, int hg) {
-  __shared__ uint16_t ks[kTileKeys * kKStride];       // key tile, row-major
+  __shared__ uint16_t ks[2 * kTileKeys * kKStride];   // two key tiles, row-major (the next one is stored during the current PV)
   __shared__ int16_t cpos[MODE == kKeysCopied ? kTopK : 1];  // kKeysCopied: list positions of the copied keys
-  __shared__ int scan_scratch[kAttnThreads / 64 + 1];
+  __shared__ int scan_scratch[kAttnWaves + 1];
+  // Partial S of each wave (its half of the dims): 8 floats per lane.
+  __shared__ float4 s_half[kAttnWaves * 64 * 2];
   // Resolved keys of the current window of kWindowTiles tiles (one per thread):
   // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to, flags.
   __shared__ int64_t win_src[kWindowKeys];
@@ -169,14 +179,34 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const int h0 = hg * kHeadsPerBlock + wave * 16;
+  const int half = wave >> 2;  // dimension half of this wave (uniform)
+  const int h0 = hg * kHeadsPerBlock + (wave & 3) * 16;
   const bool wave_active = h0 < a.heads;
   const int head = h0 + l16;
   const int64_t H = a.heads;
 
+  // Query operand of this lane, kept in registers for the whole split:
+  // head `head`, dims 288 half + 32 kk + 8 g .. +7 (16-byte chunk
+  // 4 (9 half + kk) + g of the 576), zeros for heads beyond H.  Its loads
+  // depend on nothing else, so they are issued first and land while the
+  // row plan and the first window's keys are resolved.  (An inactive row
+  // never multiplies them.)
+  uint4 qreg[kSChunks];
+  {
+    const uint4* qn = static_cast<const uint4*>(a.query) + (row * H + head) * 64;
+    const uint4* qr = static_cast<const uint4*>(a.query_rope) + (row * H + head) * 8;
+    const bool ok = wave_active && head < a.heads;
+#pragma unroll
+    for (int kk = 0; kk < kSChunks; ++kk) {
+      const int c = 4 * (kSChunks * half + kk) + g;
+      qreg[kk] = make_uint4(0, 0, 0, 0);
+      if (ok) qreg[kk] = c < 64 ? qn[c] : qr[c - 64];
+    }
+  }
+
   RowPlan plan = plan_row(a, row);
   if (MODE == kKeysCopied) {
-    // Compact the positions j < 2048 with key_src >= 0 (8 per thread, in
+    // Compact the positions j < 2048 with key_src >= 0 (4 per thread, in
     // order); the launch attends those entries only, and no tail.
     int n_copied = 0;
     if (plan.active && plan.sparse > 0) {
@@ -236,28 +266,13 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   const int my_tiles = t_first < t_end ? static_cast<int>(ceil_div(t_end - t_first, t_stride)) : 0;
 
   if (my_tiles == 0) {  // nothing for this split (whole workgroup)
-    if (wave_active && head < a.heads && g == 0) {
+    if (wave_active && head < a.heads && g == 0 && half == 0) {
       part.ml[pidx * 2 + 0] = -INFINITY;
       part.ml[pidx * 2 + 1] = 0.f;
     }
     return;
   }
 
-  // Query operand of this lane, kept in registers for the whole split:
-  // head `head`, dims 32kk + 8g .. +7 (16-byte chunk 4kk + g of the 576),
-  // zeros for heads beyond H and inactive rows.
-  uint4 qreg[kQkDim / 32];
-  auto load_queries = [&]() {
-    const uint4* qn = static_cast<const uint4*>(a.query) + (row * H + head) * 64;
-    const uint4* qr = static_cast<const uint4*>(a.query_rope) + (row * H + head) * 8;
-    const bool ok = plan.active && wave_active && head < a.heads;
-#pragma unroll
-    for (int kk = 0; kk < kQkDim / 32; ++kk) {
-      const int c = 4 * kk + g;
-      qreg[kk] = make_uint4(0, 0, 0, 0);
-      if (ok) qreg[kk] = c < 64 ? qn[c] : qr[c - 64];
-    }
-  };
 
   const int32_t* topk = a.topk_dst + row * kTopK;
   const int32_t* hbm_row_table = a.hbm_table + b * a.hbm_cols;
@@ -306,15 +321,17 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   };
   // Two mappings of a tile's 32 x 72 chunks of 16 bytes onto the threads;
   // both fill the same row-major LDS tile.
-  // * HBM tiles: thread t owns key lk = t >> 3 and its chunks lg + 8j,
-  //   lg = t & 7 (j < 8: CKV bytes [16 lg + 128 j, +16); j = 8: KPE bytes
-  //   [16 lg, +16)): one window lookup per thread and tile and immediate
-  //   offsets for the nine loads.
-  // * The fused kernel (host-sourced rows): chunk c = j * 256 + t, so a wave
-  //   instruction reads one whole 1 KiB CKV row, the request shape the host
-  //   link serves fastest.
-  const int lk = tid >> 3;
+  // * HBM tiles: thread t owns key lk = (t & 255) >> 3 and, with lg = t & 7,
+  //   the chunks lg + 8j of its row (j < 8: CKV bytes [16 lg + 128 j, +16);
+  //   j = 8: KPE bytes [16 lg, +16)): threads t < 256 take j = 0..3 and the
+  //   KPE chunk, threads t >= 256 take j = 4..7 (the split is by wave, so
+  //   uniform).  One window lookup per thread and tile, immediate offsets.
+  // * The fused kernel (host-sourced rows): chunk c = j * 512 + t (j < 5,
+  //   c < 2304), so a wave instruction reads one whole KiB of consecutive
+  //   row bytes, the request shape the host link serves fastest.
+  const int lk = (tid & 255) >> 3;
   const int lg = tid & 7;
+  constexpr int kTileChunks = kTileKeys * kChunksPerKey;  // 2304
   auto load_tile = [&](int w, bool host_tile, uint4 (&pf)[kChunksPerThread]) {
     if (FUSED && host_tile) {
       int t = tid;
@@ -322,16 +339,18 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
 #pragma unroll
       for (int jj = 0; jj < kChunksPerThread; ++jj) {
         const int cidx = jj * kAttnThreads + t;
-        const int k = cidx / kChunksPerKey;
-        const int pc = cidx - k * kChunksPerKey;
-        const int wk = w * kTileKeys + k;
-        const int flag = win_flag[wk];
-        const int64_t src = win_src[wk];
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (flag & 4) {
-          const uint4* base = (flag & 2) ? (pc < 64 ? dram_ckv + src * 64 : dram_kpe + src * 8)
-                                         : (pc < 64 ? hbm_ckv + src * 64 : hbm_kpe + src * 8);
-          v = base[pc < 64 ? pc : pc - 64];
+        if (jj < kChunksPerThread - 1 || cidx < kTileChunks) {  // (the last round: waves 0-3 only)
+          const int k = cidx / kChunksPerKey;
+          const int pc = cidx - k * kChunksPerKey;
+          const int wk = w * kTileKeys + k;
+          const int flag = win_flag[wk];
+          const int64_t src = win_src[wk];
+          if (flag & 4) {
+            const uint4* base = (flag & 2) ? (pc < 64 ? dram_ckv + src * 64 : dram_kpe + src * 8)
+                                           : (pc < 64 ? hbm_ckv + src * 64 : hbm_kpe + src * 8);
+            v = base[pc < 64 ? pc : pc - 64];
+          }
         }
         pf[jj] = v;
       }
@@ -340,27 +359,27 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     const int wk = w * kTileKeys + lk;
     const int flag = win_flag[wk];
     const int64_t src = win_src[wk];
-    const uint4* ckv = hbm_ckv + src * 64 + lg;
-    const uint4* kpe = hbm_kpe + src * 8 + lg;
+    const uint4* ckv = hbm_ckv + src * 64 + lg + 32 * half;
     if (flag & 4) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = ckv[8 * j];
-      pf[8] = kpe[0];
+      for (int j = 0; j < 4; ++j) pf[j] = ckv[8 * j];
+      pf[4] = half == 0 ? hbm_kpe[src * 8 + lg] : make_uint4(0, 0, 0, 0);
     } else {
 #pragma unroll
       for (int j = 0; j < kChunksPerThread; ++j) pf[j] = make_uint4(0, 0, 0, 0);
     }
   };
-  auto store_tile = [&](int w, bool host_tile, const uint4 (&pf)[kChunksPerThread]) {
+  auto store_tile = [&](int w, bool host_tile, const uint4 (&pf)[kChunksPerThread], uint16_t* kt_base) {
     if (FUSED && host_tile) {
       int t = tid;
       asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
       for (int jj = 0; jj < kChunksPerThread; ++jj) {
         const int cidx = jj * kAttnThreads + t;
+        if (jj == kChunksPerThread - 1 && cidx >= kTileChunks) break;
         const int k = cidx / kChunksPerKey;
         const int pc = cidx - k * kChunksPerKey;
-        *reinterpret_cast<uint4*>(&ks[k * kKStride + pc * 8]) = pf[jj];
+        *reinterpret_cast<uint4*>(&kt_base[k * kKStride + pc * 8]) = pf[jj];
         const int wk = w * kTileKeys + k;
         if (win_flag[wk] & 2) {  // a host-sourced miss: persist it to its HBM slot
           const int64_t dst = win_dst[wk];
@@ -372,58 +391,90 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
       }
       return;
     }
-    uint16_t* rowp = &ks[lk * kKStride + lg * 8];
+    uint16_t* rowp = &kt_base[lk * kKStride + lg * 8 + 256 * half];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4*>(rowp + 64 * j) = pf[j];
-    *reinterpret_cast<uint4*>(rowp + kCkvDim) = pf[8];
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(rowp + 64 * j) = pf[j];
+    if (half == 0) *reinterpret_cast<uint4*>(&kt_base[lk * kKStride + kCkvDim + lg * 8]) = pf[4];
   };
 
-  // The first tile's loads (possibly host rows) are issued before the
-  // query loads.
   // The fused kernel reads every tile row per wave: with the key-per-8-lanes
   // mapping on its HBM tiles, the host link under them served the miss tiles
   // more slowly (cfg1 fused kernel 129 -> 138 us).
   auto is_host_tile = [&](int, int) { return FUSED; };
   uint4 pf[kChunksPerThread];
-  resolve_window(0);
-  __syncthreads();
-  load_tile(0, is_host_tile(0, 0), pf);
-  load_queries();
 
   const float qscale = a.scale * kLog2e;
+  const bool compute = wave_active && plan.active;  // uniform per wave, equal within a pair
   float m_run = -INFINITY;  // running max (base-2 logits) of head `head`
   float l_run = 0.f;        // this lane's share of the running sum
-  f32x4_t oacc[kCkvDim / 16];
+  f32x4_t oacc[kVDims / 16];
 #pragma unroll
-  for (int i = 0; i < kCkvDim / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < kVDims / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float4* my_s = &s_half[(wave * 64 + lane) * 2];
+  const float4* pair_s = &s_half[((wave ^ 4) * 64 + lane) * 2];
 
+  // Per tile two barriers: (S halves written) and (next tile stored, this
+  // tile's PV done).  Tile w sits in buffer w & 1; tile w + 1 is loaded
+  // during S(w) and stored into the other buffer after PV(w)'s reads.
   for (int first = 0; first < my_tiles; first += kWindowTiles) {
-    if (first > 0) {
-      resolve_window(first);
-      __syncthreads();
-      load_tile(0, is_host_tile(first, 0), pf);
-    }
+    resolve_window(first);
+    __syncthreads();
+    load_tile(0, is_host_tile(first, 0), pf);
+    store_tile(0, is_host_tile(first, 0), pf, ks);
+    __syncthreads();
     const int wtiles = min(kWindowTiles, my_tiles - first);
     for (int w = 0; w < wtiles; ++w) {
-      store_tile(w, is_host_tile(first, w), pf);
-      __syncthreads();                     // tile w resident in LDS
-      if (w + 1 < wtiles) load_tile(w + 1, is_host_tile(first, w + 1), pf);  // in flight during the MFMA work below
+      uint16_t* kcur = ks + (w & 1) * (kTileKeys * kKStride);
+      uint16_t* knext = ks + ((w + 1) & 1) * (kTileKeys * kKStride);
+      if (w + 1 < wtiles) load_tile(w + 1, is_host_tile(first, w + 1), pf);  // in flight during S and PV below
 
-      if (wave_active && plan.active) {
-        // S^T tile: two 16-key blocks; lane holds S[head][kt*16 + 4g + i].
-        f32x4_t sacc[2];
+      // This wave's half of the S^T tile: two 16-key blocks; lane holds
+      // the partial S[head][kt*16 + 4g + i] over dims [288 half, +288).
+      f32x4_t sacc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+      if (compute) {
+        // Every operand read is issued before the first MFMA (18 reads in
+        // flight instead of a read-wait-multiply chain).
+        const uint16_t* krow = &kcur[l16 * kKStride + 288 * half + g * 8];
+        uint4 kf[2][kSChunks];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          const uint16_t* krow = &ks[(kt * 16 + l16) * kKStride + g * 8];
+        for (int kk = 0; kk < kSChunks; ++kk)
 #pragma unroll
-          for (int kk = 0; kk < kQkDim / 32; ++kk) {
-            const uint4 kf = *reinterpret_cast<const uint4*>(krow + kk * 32);
-            acc = T::mfma16(__builtin_bit_cast(typename T::vec8, kf), __builtin_bit_cast(typename T::vec8, qreg[kk]), acc);
-            if ((kk & 5) == 5) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
-          }
-          sacc[kt] = acc;
+          for (int kt = 0; kt < 2; ++kt) kf[kt][kk] = *reinterpret_cast<const uint4*>(krow + kt * 16 * kKStride + kk * 32);
+#pragma unroll
+        for (int kk = 0; kk < kSChunks; ++kk)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+            sacc[kt] = T::mfma16(__builtin_bit_cast(typename T::vec8, kf[kt][kk]),
+                                 __builtin_bit_cast(typename T::vec8, qreg[kk]), sacc[kt]);
+        // (The scheduler otherwise interleaves them back to two in flight.)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kSChunks, 0);  // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * kSChunks, 0);  // MFMAs
+        my_s[0] = make_float4(sacc[0][0], sacc[0][1], sacc[0][2], sacc[0][3]);
+        my_s[1] = make_float4(sacc[1][0], sacc[1][1], sacc[1][2], sacc[1][3]);
+      }
+      __syncthreads();  // both halves of S written
+
+      if (compute) {
+        // The V^T operands of the whole tile are read first, so their LDS
+        // latency passes under the softmax.  A operand V^T[dim][key] from the
+        // row-major tile: keys 4g..4g+3 and 16+4g..16+4g+3 (the lanes' S^T
+        // columns) at dim 256 half + dt*16 + l16, each 4-key group one
+        // transposing LDS read (lane i of a 16-lane group reads dims
+        // 4(i&3)..+3 of key i>>2; lane l receives the four keys' values at
+        // dim l).
+        const uint16_t* v0 = &kcur[(4 * g + (l16 >> 2)) * kKStride + kVDims * half + 4 * (l16 & 3)];
+        const uint16_t* v1 = v0 + 16 * kKStride;
+        uint2 vlo[kVDims / 16], vhi[kVDims / 16];
+#pragma unroll
+        for (int dt = 0; dt < kVDims / 16; ++dt) {
+          vlo[dt] = lds_read_tr16(v0 + dt * 16);
+          vhi[dt] = lds_read_tr16(v1 + dt * 16);
         }
+        // S = own half + the pair's half (addition commutes: both waves of
+        // the pair hold the same S).
+        const float4 o0 = pair_s[0], o1 = pair_s[1];
+        const float st[8] = {sacc[0][0] + o0.x, sacc[0][1] + o0.y, sacc[0][2] + o0.z, sacc[0][3] + o0.w,
+                             sacc[1][0] + o1.x, sacc[1][1] + o1.y, sacc[1][2] + o1.z, sacc[1][3] + o1.w};
         float sv[8];
         float mx = -INFINITY;
 #pragma unroll
@@ -431,7 +482,7 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int k = kt * 16 + 4 * g + i;
-            const float x = (win_flag[w * kTileKeys + k] & 1) ? sacc[kt][i] * qscale : -INFINITY;
+            const float x = (win_flag[w * kTileKeys + k] & 1) ? st[kt * 4 + i] * qscale : -INFINITY;
             sv[kt * 4 + i] = x;
             mx = fmaxf(mx, x);
           }
@@ -440,87 +491,79 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
         // The reference max only moves when the tile max exceeds it by more
         // than kMaxSlack (base-2 units), so P stays below 2^kMaxSlack and the
         // numerator is rescaled on few tiles (softmax does not depend on the
-        // subtracted constant).
+        // subtracted constant).  While no key has been attended (m_run and
+        // the tile max -inf) the subtracted constant is 0: P, the sum and
+        // alpha are then all 0 and the tile adds nothing.
         const bool grow = mx > m_run + kMaxSlack;  // also m_run == -inf with a finite tile max
         const float m_new = grow ? mx : m_run;
-        if (m_new != -INFINITY) {
-          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 1 unless grow; 0 from m_run == -inf
-          const bool rescale = __any(grow && m_run != -INFINITY);  // (zero numerators need none)
-          m_run = m_new;
-          float psum = 0.f;
-          float p[8];
+        const float m_sub = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);  // 1 unless grow; 0 from m_run == -inf
+        const bool rescale = __any(grow && m_run != -INFINITY);     // (zero numerators need none)
+        m_run = m_new;
+        float psum = 0.f;
+        float p[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(sv[i] - m_new);  // (results below 2^-126 flush to 0)
-            psum += p[i];
-          }
-          l_run = l_run * alpha + psum;
-          if (rescale) {
+        for (int i = 0; i < 8; ++i) {
+          p[i] = __builtin_amdgcn_exp2f(sv[i] - m_sub);  // (results below 2^-126 flush to 0)
+          psum += p[i];
+        }
+        l_run = l_run * alpha + psum;
+        if (rescale) {
 #pragma unroll
-            for (int dt = 0; dt < kCkvDim / 16; ++dt) {
-              oacc[dt][0] *= alpha;
-              oacc[dt][1] *= alpha;
-              oacc[dt][2] *= alpha;
-              oacc[dt][3] *= alpha;
-            }
-          }
-          // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
-          // ~16 mantissa bits of P instead of 8.  (One rounded P is not
-          // enough: with near-uniform attention over thousands of keys the
-          // output is a small mean of zero-mean rows, and P's rounding error
-          // does not shrink with it.)
-          typename T::vec8 pb_hi, pb_lo;
-          uint16_t* phs = reinterpret_cast<uint16_t*>(&pb_hi);
-          uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            phs[i] = T::hi_part(p[i]);
-            pls[i] = T::from_finite(p[i] - T::to_float(phs[i]));
-          }
-          // A operand V^T[dim][key] from the row-major tile: keys 4g..4g+3
-          // and 16+4g..16+4g+3 (the lanes' S^T columns) at dim dt*16 + l16,
-          // each 4-key group one transposing LDS read (lane i of a 16-lane
-          // group reads dims 4(i&3)..+3 of key i>>2; lane l receives the
-          // four keys' values at dim l).
-          const uint16_t* v0 = &ks[(4 * g + (l16 >> 2)) * kKStride + 4 * (l16 & 3)];
-          const uint16_t* v1 = &ks[(16 + 4 * g + (l16 >> 2)) * kKStride + 4 * (l16 & 3)];
-#pragma unroll
-          for (int dt = 0; dt < kCkvDim / 16; ++dt) {
-            const uint2 lo = lds_read_tr16(v0 + dt * 16);
-            const uint2 hi = lds_read_tr16(v1 + dt * 16);
-            const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            oacc[dt] = T::mfma16(af, pb_lo, T::mfma16(af, pb_hi, oacc[dt]));
-            if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound operand hoisting (registers)
+          for (int dt = 0; dt < kVDims / 16; ++dt) {
+            oacc[dt][0] *= alpha;
+            oacc[dt][1] *= alpha;
+            oacc[dt][2] *= alpha;
+            oacc[dt][3] *= alpha;
           }
         }
-        // The numerators live in accumulation registers across tiles (the
-        // rare rescale above copies them out and back).
+        // P as a hi + lo pair of 16-bit values: two MFMAs give P . V with
+        // ~16 mantissa bits of P instead of 8.  (One rounded P is not
+        // enough: with near-uniform attention over thousands of keys the
+        // output is a small mean of zero-mean rows, and P's rounding error
+        // does not shrink with it.)
+        typename T::vec8 pb_hi, pb_lo;
+        uint16_t* phs = reinterpret_cast<uint16_t*>(&pb_hi);
+        uint16_t* pls = reinterpret_cast<uint16_t*>(&pb_lo);
 #pragma unroll
-        for (int dt = 0; dt < kCkvDim / 16; ++dt) asm volatile("" : "+a"(oacc[dt]));
+        for (int i = 0; i < 8; ++i) {
+          phs[i] = T::hi_part(p[i]);
+          pls[i] = T::from_finite(p[i] - T::to_float(phs[i]));
+        }
+#pragma unroll
+        for (int dt = 0; dt < kVDims / 16; ++dt) {
+          const auto af = __builtin_bit_cast(typename T::vec8, make_uint4(vlo[dt].x, vlo[dt].y, vhi[dt].x, vhi[dt].y));
+          oacc[dt] = T::mfma16(af, pb_lo, T::mfma16(af, pb_hi, oacc[dt]));
+        }
       }
-      __syncthreads();  // every wave is done with ks before the next store
+      if (w + 1 < wtiles) store_tile(w + 1, is_host_tile(first, w + 1), pf, knext);
+      __syncthreads();  // tile w + 1 resident; every wave done with tile w and s_half
     }
   }
 
-  // Split partials: max, sum and un-normalised numerator per head.
+  // Split partials: max, sum and un-normalised numerator per head (each
+  // wave its 256 latent dims; the pair's (max, sum) are equal, half 0
+  // writes them).
   if (!wave_active || head >= a.heads) return;
   float lsum = l_run + __shfl_xor(l_run, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
-  if (g == 0) {
+  if (g == 0 && half == 0) {
     part.ml[pidx * 2 + 0] = m_run;
     part.ml[pidx * 2 + 1] = lsum;
   }
   if (lsum > 0.f) {
-    float* od = part.o + pidx * kCkvDim;
+    float* od = part.o + pidx * kCkvDim + kVDims * half;
 #pragma unroll
-    for (int dt = 0; dt < kCkvDim / 16; ++dt)
+    for (int dt = 0; dt < kVDims / 16; ++dt)
       *reinterpret_cast<float4*>(od + dt * 16 + 4 * g) =
           make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
   }
 }
 
+// Two waves per SIMD (one 512-thread workgroup per CU): the compiler may use
+// up to 256 registers per lane and schedule for latency, not occupancy.
 template <typename T, bool FUSED, int MODE>
-__global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Partials part, int splits, int split_base,
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void sfa_split_kernel(SfaArgs a, Partials part, int splits, int split_base,
                                                                  int splits_total) {
   sfa_split_body<T, FUSED, MODE>(a, part, splits, split_base, splits_total, blockIdx.x, blockIdx.y);
 }
@@ -534,15 +577,17 @@ __global__ __launch_bounds__(kAttnThreads) void sfa_split_kernel(SfaArgs a, Part
 // No workgroup waits on another: the copied keys are attended by a second
 // launch on the same stream.
 template <typename T>
-__global__ __launch_bounds__(kAttnThreads) void sfa_mtp_overlap_kernel(SfaArgs a, Partials part, int splits,
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void sfa_mtp_overlap_kernel(SfaArgs a, Partials part, int splits,
                                                                        int splits_total, ScatterArgs sc,
                                                                        int attn_blocks, int hgroups, int copy_wgs) {
   const int p = blockIdx.x;
   const int xcd = p & 7;
   const int slot = p >> 3;
   if (xcd < kCopyXcds) {
+    // The copy moves 16-pair chunks with 4 waves (scatter_copy_wg); the
+    // workgroup's other waves have nothing to copy.
     const int wg = slot * kCopyXcds + xcd;
-    if (wg < copy_wgs) scatter_copy_wg(sc, wg, copy_wgs);
+    if (wg < copy_wgs && threadIdx.x < 256) scatter_copy_wg(sc, wg, copy_wgs);
     return;
   }
   const int i = slot * (8 - kCopyXcds) + (xcd - kCopyXcds);
