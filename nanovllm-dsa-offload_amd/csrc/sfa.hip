@@ -169,7 +169,7 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to, flags.
   __shared__ int64_t win_src[kWindowKeys];
   __shared__ int64_t win_dst[kWindowKeys];
-  __shared__ int win_flag[kWindowKeys];  // bit 0: attend, bit 1: source is DRAM, bit 2: source valid
+  __shared__ __align__(16) int win_flag[kWindowKeys];  // bit 0: attend, bit 1: source is DRAM, bit 2: source valid
 
   const int64_t row = bid / splits;
   const int split = static_cast<int>(bid - row * splits);
@@ -462,6 +462,10 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
         // transposing LDS read (lane i of a 16-lane group reads dims
         // 4(i&3)..+3 of key i>>2; lane l receives the four keys' values at
         // dim l).
+        const float4 o0 = pair_s[0], o1 = pair_s[1];
+        const int4 f0 = *reinterpret_cast<const int4*>(&win_flag[w * kTileKeys + 4 * g]);
+        const int4 f1 = *reinterpret_cast<const int4*>(&win_flag[w * kTileKeys + 16 + 4 * g]);
+        const int fl[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
         const uint16_t* v0 = &kcur[(4 * g + (l16 >> 2)) * kKStride + kVDims * half + 4 * (l16 & 3)];
         const uint16_t* v1 = v0 + 16 * kKStride;
         uint2 vlo[kVDims / 16], vhi[kVDims / 16];
@@ -472,7 +476,6 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
         }
         // S = own half + the pair's half (addition commutes: both waves of
         // the pair hold the same S).
-        const float4 o0 = pair_s[0], o1 = pair_s[1];
         const float st[8] = {sacc[0][0] + o0.x, sacc[0][1] + o0.y, sacc[0][2] + o0.z, sacc[0][3] + o0.w,
                              sacc[1][0] + o1.x, sacc[1][1] + o1.y, sacc[1][2] + o1.z, sacc[1][3] + o1.w};
         float sv[8];
@@ -482,7 +485,7 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int k = kt * 16 + 4 * g + i;
-            const float x = (win_flag[w * kTileKeys + k] & 1) ? st[kt * 4 + i] * qscale : -INFINITY;
+            const float x = (fl[kt * 4 + i] & 1) ? st[kt * 4 + i] * qscale : -INFINITY;
             sv[kt * 4 + i] = x;
             mx = fmaxf(mx, x);
           }
