@@ -599,35 +599,43 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   sfa_split_body<T, false, kKeysResident>(a, part, splits, 0, splits_total, i % attn_blocks, i / attn_blocks);
 }
 
-// Merge split partials: one 128-thread workgroup per (row, head), 4 of the
-// 512 latent dims per thread.  Lane s of each wave reads split s's (m, l)
-// (and split s + 64's), so the running max, the weights exp2(m_s - max) and
-// the softmax denominator come from one load and two wave reductions.  The
-// output slices are loaded kCombineBatch splits at a time, all in flight
-// together (the first batch is issued before the reductions), and summed in
-// split order.  Splits with l == 0 hold no keys and are skipped.  A small
-// batch launches many splits per row (e.g. 32 at 8 rows), which a chain of
-// one dependent load per split would turn into a latency-bound merge.
+// Merge split partials: one workgroup per (row, head) of G groups of 128
+// threads, 4 of the 512 latent dims per thread; group g merges the splits
+// [16g, 16g + 16) (G = ceil(splits / 16), at most 8), so every thread loads
+// its output slices in one round, all in flight together.  Lane s of each
+// wave reads split s's (m, l) (and split s + 64's), so the running max, the
+// weights exp2(m_s - max) and the softmax denominator come from one load and
+// two wave reductions (every wave computes them).  Within a group the slices
+// are summed in split order; the groups' sums are then added in group order
+// through LDS.  Splits with l == 0 hold no keys and are skipped.  (A chain of
+// one dependent load per split, or one group walking 64 splits 16 at a time,
+// is latency-bound: a single row launches 64 splits.)
 constexpr int kCombineBatch = 16;
 constexpr int kCombineMaxSplits = 2 * kWave;
+constexpr int kCombineMaxGroups = kCombineMaxSplits / kCombineBatch;  // 8
 static_assert(2 * kMaxSplits <= kCombineMaxSplits, "an MTP3 launch pair merges up to 2 x kMaxSplits splits");
 
 template <typename T>
-__global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
+__global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
+  __shared__ float4 gsum[kCombineMaxGroups - 1][128];
   const int64_t H = a.heads;
   const int lane = threadIdx.x & (kWave - 1);
+  const int grp = threadIdx.x >> 7;  // split group (uniform per wave)
+  const int dq = threadIdx.x & 127;  // dims 4 dq .. 4 dq + 3
+  const int groups = blockDim.x >> 7;
   // The partial of (row, split s, head) sits at index base + s * H.
   const int64_t base = static_cast<int64_t>(blockIdx.x) * splits * H + blockIdx.y;
   const float2* mlp = reinterpret_cast<const float2*>(part.ml);
   const float4* op = reinterpret_cast<const float4*>(part.o);
   constexpr int kVec = kCkvDim / 4;
-  float2 v0 = make_float2(0.f, 0.f), v1 = v0;
-  if (lane < splits) v0 = mlp[base + lane * H];
-  if (lane + kWave < splits) v1 = mlp[base + (lane + kWave) * H];
+  const int s0 = grp * kCombineBatch;
   float4 x[kCombineBatch];
 #pragma unroll
   for (int j = 0; j < kCombineBatch; ++j)  // an index past the last split rereads it (ignored below)
-    x[j] = op[(base + min(j, splits - 1) * H) * kVec + threadIdx.x];
+    x[j] = op[(base + min(s0 + j, splits - 1) * H) * kVec + dq];
+  float2 v0 = make_float2(0.f, 0.f), v1 = v0;
+  if (lane < splits) v0 = mlp[base + lane * H];
+  if (lane + kWave < splits) v1 = mlp[base + (lane + kWave) * H];
   const bool live0 = v0.y > 0.f, live1 = v1.y > 0.f;
   float m = fmaxf(live0 ? v0.x : -INFINITY, live1 ? v1.x : -INFINITY);
 #pragma unroll
@@ -640,32 +648,37 @@ __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials pa
   float total = (live0 ? v0.y * w0 : 0.f) + (live1 ? v1.y * w1 : 0.f);
 #pragma unroll
   for (int off = kWave / 2; off >= 1; off >>= 1) total += __shfl_xor(total, off, kWave);
+  // Consumed here, unconditionally: otherwise the compiler sinks each
+  // split's load into its conditional use below, one wait each.
+#pragma unroll
+  for (int j = 0; j < kCombineBatch; ++j) asm volatile("" : "+v"(x[j].x), "+v"(x[j].y), "+v"(x[j].z), "+v"(x[j].w));
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < splits; s0 += kCombineBatch) {
-    if (s0 > 0) {
 #pragma unroll
-      for (int j = 0; j < kCombineBatch; ++j)
-        x[j] = op[(base + min(s0 + j, splits - 1) * H) * kVec + threadIdx.x];
+  for (int j = 0; j < kCombineBatch; ++j) {
+    const int sp = s0 + j;  // uniform
+    const float ws = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sp < kWave ? w0 : w1), sp & (kWave - 1)));
+    if (sp < splits && ws != 0.f) {
+      acc.x += x[j].x * ws;
+      acc.y += x[j].y * ws;
+      acc.z += x[j].z * ws;
+      acc.w += x[j].w * ws;
     }
-    // Consumed here, unconditionally: otherwise the compiler sinks each
-    // split's load into its conditional use below, one wait each.
-#pragma unroll
-    for (int j = 0; j < kCombineBatch; ++j) asm volatile("" : "+v"(x[j].x), "+v"(x[j].y), "+v"(x[j].z), "+v"(x[j].w));
-#pragma unroll
-    for (int j = 0; j < kCombineBatch; ++j) {
-      const int s = s0 + j;  // uniform
-      const float ws = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s < kWave ? w0 : w1), s & (kWave - 1)));
-      if (s < splits && ws != 0.f) {
-        acc.x += x[j].x * ws;
-        acc.y += x[j].y * ws;
-        acc.z += x[j].z * ws;
-        acc.w += x[j].w * ws;
-      }
+  }
+  if (groups > 1) {
+    if (grp > 0) gsum[grp - 1][dq] = acc;
+    __syncthreads();
+    if (grp > 0) return;
+    for (int g2 = 1; g2 < groups; ++g2) {
+      const float4 o = gsum[g2 - 1][dq];
+      acc.x += o.x;
+      acc.y += o.y;
+      acc.z += o.z;
+      acc.w += o.w;
     }
   }
   const float inv = total > 0.f ? 1.f / total : 0.f;
-  uint16_t* out = static_cast<uint16_t*>(a.out) + (blockIdx.x * H + blockIdx.y) * kCkvDim + threadIdx.x * 4;
+  uint16_t* out = static_cast<uint16_t*>(a.out) + (blockIdx.x * H + blockIdx.y) * kCkvDim + dq * 4;
   const uint32_t lo = static_cast<uint32_t>(T::from_float(acc.x * inv)) |
                       (static_cast<uint32_t>(T::from_float(acc.y * inv)) << 16);
   const uint32_t hi = static_cast<uint32_t>(T::from_float(acc.z * inv)) |
@@ -676,7 +689,8 @@ __global__ __launch_bounds__(128) void sfa_combine_kernel(SfaArgs a, Partials pa
 template <typename T>
 void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int splits, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads));
-  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>, grid, dim3(128), stream, a, p, splits);
+  const int groups = std::min<int>(kCombineMaxGroups, std::max<int>(1, static_cast<int>(ceil_div(splits, kCombineBatch))));
+  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>, grid, dim3(128 * groups), stream, a, p, splits);
 }
 
 template <typename T, bool FUSED>
