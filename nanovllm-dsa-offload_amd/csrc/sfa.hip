@@ -249,10 +249,13 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     // at least kMissSplits per row (measured best at 24 rows; more of them
     // leave too few splits for the row's HBM-resident tiles), more per row at
     // small batches (4 at 8 rows: 3% off the 78-layer step), never more than
-    // the row's miss tiles.
+    // the row's miss tiles.  A row with more than 4 miss tiles per miss split
+    // gets a third one when it has at least 6 splits: its miss workgroups
+    // were the launch's last to finish (24 rows: fused kernel -0.8 us).
     int miss_splits = static_cast<int>(ceil_div(kMissWorkgroups, a.batch * a.rows_per_request));
     if (miss_splits > mtiles) miss_splits = mtiles;
     if (miss_splits < kMissSplits) miss_splits = kMissSplits;
+    if (splits >= 6 && mtiles > 4 * kMissSplits && miss_splits < 3) miss_splits = 3;
     if (miss_splits > splits - 1) miss_splits = splits - 1;
     if (split < miss_splits) {
       t_first = split;
