@@ -30,14 +30,15 @@
 //   kernel merges the per-split (max, sum, numerator) partials.
 //   fused_copy_sfa (MTP0): a row's miss keys are the first miss_counts
 //   entries of its list.  The first few splits of the row (kMissSplits, more
-//   at small batches) take the tiles holding them: each such tile is read
-//   once from host-mapped DRAM,
-//   stored to its HBM slots and consumed from LDS.  A split's host tiles are
-//   sequential (one PCIe round trip each).  The other splits take the
-//   HBM-only tiles, so the host-link-bound copy and the HBM-bound attention
-//   run side by side.  fused_copy_sfa_mtp: the union misses are
-//   not tile-aligned to any one query row, so the union is copied first
-//   (scatter_copy) and the MTP attention follows on the same stream.
+//   at small batches and for rows with many misses) take the tiles holding
+//   them: each such tile is read once from host-mapped DRAM, stored to its
+//   HBM slots and consumed from LDS.  A split's host tiles are sequential
+//   (one PCIe round trip each).  The other splits take the HBM-only tiles,
+//   so the host-link-bound copy and the HBM-bound attention run side by
+//   side.  fused_copy_sfa_mtp: the union misses are not tile-aligned to any
+//   one query row, so one launch copies the union on some XCDs while the
+//   others attend the keys already in HBM, and a second launch attends the
+//   copied keys.
 #include <algorithm>
 #include <cfloat>
 
