@@ -210,10 +210,16 @@ def test_fused_copy_sfa_c0_row_and_serial_pair():
     torch.testing.assert_close(out.float(), out2.float(), rtol=0.02, atol=0.01)
 
 
-def test_fused_copy_sfa_mtp_matches_composition():
+# One request: 4 query rows, 48 + 64 splits over the two attention launches,
+# merged by seven 16-split groups of the combine; two requests: 56 splits.
+@pytest.mark.parametrize("batch", [2, 1])
+def test_fused_copy_sfa_mtp_matches_composition(batch):
     from nanovllm_amd.workloads import make_chain_case
 
-    case = make_chain_case(2, [9216, 12288], [8192, 9216], [4, 33], seed=8, mtp=True)
+    if batch == 2:
+        case = make_chain_case(2, [9216, 12288], [8192, 9216], [4, 33], seed=8, mtp=True)
+    else:
+        case = make_chain_case(1, [12288], [8192], [33], seed=9, mtp=True)
     case = _chain_after_lim(case, mtp=True)
     gold, hkpe, hckv = _oracle_fused(case, mtp=True)
     d = case.to_device("cuda")
