@@ -671,10 +671,12 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
                                t["hbm_block_table"], t["dram_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"],
                                t["dram_k_rope"], t["dram_kv_cache"], case.meta["scale"], t["attention_out"])
 
+    _lib.xcd_roles(reset=True)
     for _ in range(2):
         t["cache_slots_pool"].copy_(pool0)
         step()
-    torch.cuda.synchronize()
+    # the XCDs the overlap kernel's copy and attention workgroups ran on in the two warm-up steps
+    copy_xcds, attn_xcds = _lib.xcd_roles(reset=True)
     times = []
     with _lib.KernelTimer(capacity=16 * reps) as kt:
         for _ in range(reps):
@@ -698,6 +700,8 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
     out = {"workload": "bs=16 x 4 queries, prompts 49152, C=8192, tails U[4,127], HIP-graph replay",
            "step_us": round(graph_us, 2), "eager_step_us": round(step_us, 2),
            "union_misses_per_step": misses, "kernels_us": km,
+           "xcd_roles": {"copy": f"{copy_xcds:#04x}", "attention": f"{attn_xcds:#04x}",
+                         "disjoint": (copy_xcds & attn_xcds) == 0},
            "lim_score_hbm_GBs": round(score_bytes / (km["lim_score_kernel"] * 1e-6) / 1e9, 1),
            # the overlap kernel copies the union misses while attending the HBM-resident keys
            "copy_h2d_GBs": round(misses * ROW_BYTES / (km["sfa_mtp_overlap_kernel"] * 1e-6) / 1e9, 2),

@@ -390,6 +390,20 @@ int nvdsa_profile_begin(int32_t capacity);
 int nvdsa_profile_end(float* durations_ms, int32_t* kernel_ids, int32_t capacity, int32_t* recorded);
 const char* nvdsa_kernel_name(int32_t kernel_id);
 
+/* ---------------------------------------------------------------------- */
+/* Dispatch check (diagnostics; no counterpart in the reference).  The first
+ * kernel of nvdsa_fused_copy_sfa_mtp gives workgroups the copy role or the
+ * attention role by linear id, assuming the dispatcher deals workgroups to
+ * the 8 XCDs round-robin (single-partition mode), so that the host reads of
+ * the copy never share an XCD with the attention's HBM reads.  Each of its
+ * workgroups records the XCD it ran on: bit x of masks[0] is set when a copy
+ * workgroup ran on XCD x, of masks[1] when an attention workgroup did,
+ * accumulated on the current device since the last reset.  The masks are
+ * disjoint when the assumption held.  Results are correct either way; only
+ * the speed depends on it.  With reset != 0 the record is cleared after the
+ * read.  Synchronises the device; not for use under graph capture. */
+int nvdsa_xcd_roles(uint32_t* masks, int32_t reset);
+
 #ifdef __cplusplus
 }
 #endif

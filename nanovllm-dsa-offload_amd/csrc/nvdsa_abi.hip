@@ -190,6 +190,16 @@ const char* nvdsa_kernel_name(int32_t kernel_id) {
   return names[kernel_id];
 }
 
+int nvdsa_xcd_roles(uint32_t* masks, int32_t reset) {
+  if (masks == nullptr) return fail(NVDSA_ERR_ARG, "xcd_roles: masks must not be null");
+  const hipError_t err = nvdsa::sfa_xcd_roles(masks, reset != 0);
+  if (err != hipSuccess) {
+    g_last_error = std::string("xcd_roles: ") + hipGetErrorString(err);
+    return NVDSA_ERR_RUNTIME;
+  }
+  return NVDSA_OK;
+}
+
 const char* nvdsa_last_error(void) { return g_last_error.c_str(); }
 
 const char* nvdsa_version(void) { return "nvdsa 0.1.0 gfx950"; }

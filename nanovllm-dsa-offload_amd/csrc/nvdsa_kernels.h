@@ -178,6 +178,10 @@ struct SfaArgs {
 size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens);
 hipError_t launch_sparse_tail_attention(const SfaArgs& a, hipStream_t stream);
 hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream);
+// Copies the current device's record of the XCDs the MTP3 overlap kernel's
+// copy ([0]) and attention ([1]) workgroups ran on; clears it after the read
+// when `reset`.  Synchronises the device.
+hipError_t sfa_xcd_roles(uint32_t masks[2], bool reset);
 
 // ---- indexer projection (decode query rows and head weights) -------------
 struct IndexerArgs {

@@ -131,6 +131,20 @@ Partials carve(void* ws, int64_t rows, int64_t splits, int64_t heads) {
 // workgroup per CU.
 constexpr int kCopyXcds = 5;
 constexpr int kCopyWgs = kCopyXcds * 32;
+
+// The XCDs each role of sfa_mtp_overlap_kernel ran on since the last reset
+// (bit x of [0]: a copy workgroup ran on XCD x; of [1]: an attention
+// workgroup), one copy per device, read by sfa_xcd_roles.  The roles are
+// given by linear workgroup id on the assumption that the dispatcher deals
+// workgroups to the XCDs round-robin; the masks show whether it did.
+__device__ unsigned int g_xcd_roles[2];
+
+// Id of the XCD the calling wave runs on (hardware register XCC_ID, bits 3:0).
+__device__ inline unsigned int hw_xcd_id() {
+  unsigned int v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+  return v;
+}
 int overlap_splits(int64_t rows, int64_t head_groups) {
   // About two workgroups per attention CU: the rows' tiles spread evenly.
   int64_t s = ceil_div(2 * (8 - kCopyXcds) * 32, rows * head_groups);
@@ -591,6 +605,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   const int p = blockIdx.x;
   const int xcd = p & 7;
   const int slot = p >> 3;
+  if (threadIdx.x == 0) atomicOr(&g_xcd_roles[xcd < kCopyXcds ? 0 : 1], 1u << hw_xcd_id());
   if (xcd < kCopyXcds) {
     // The copy moves 16-pair chunks with 4 waves (scatter_copy_wg); the
     // workgroup's other waves have nothing to copy.
@@ -787,6 +802,16 @@ hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream) {
   if (a.rows_per_request > 1)  // MTP3: the union misses are not tile-aligned to any one query row
     return a.elem == Elem::kBf16 ? launch_fused_mtp<Bf16>(a, stream) : launch_fused_mtp<F16>(a, stream);
   return a.elem == Elem::kBf16 ? launch_sfa<Bf16, true>(a, stream) : launch_sfa<F16, true>(a, stream);
+}
+
+hipError_t sfa_xcd_roles(uint32_t masks[2], bool reset) {
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess) err = hipMemcpyFromSymbol(masks, HIP_SYMBOL(g_xcd_roles), sizeof(g_xcd_roles));
+  if (err == hipSuccess && reset) {
+    const unsigned int zero[2] = {0u, 0u};
+    err = hipMemcpyToSymbol(HIP_SYMBOL(g_xcd_roles), zero, sizeof(zero));
+  }
+  return err;
 }
 
 }  // namespace nvdsa

@@ -79,6 +79,7 @@ SIGNATURES = {
     "nvdsa_profile_end": ([ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int32), ctypes.c_int32,
                            ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
     "nvdsa_kernel_name": ([ctypes.c_int32], ctypes.c_char_p),
+    "nvdsa_xcd_roles": ([ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32], ctypes.c_int),
 }
 
 
@@ -169,6 +170,17 @@ class KernelTimer:
     def mean_ms(self, name: str) -> float:
         vals = [ms for k, ms in self.records if k == name]
         return sum(vals) / len(vals) if vals else float("nan")
+
+
+def xcd_roles(reset: bool = False) -> tuple[int, int]:
+    """(copy, attention) bit masks of the XCDs the MTP3 overlap kernel's two
+    workgroup roles ran on, on the current device, since the last reset
+    (nvdsa_xcd_roles).  Disjoint masks mean the dispatcher dealt workgroups to
+    the XCDs round-robin, as the kernel's role split assumes.  Synchronises
+    the device."""
+    masks = (ctypes.c_uint32 * 2)()
+    check(lib.nvdsa_xcd_roles(masks, int(reset)))
+    return int(masks[0]), int(masks[1])
 
 
 def exported_symbols_from_header(header: os.PathLike | str) -> list[str]:

@@ -227,3 +227,26 @@ def test_fused_copy_sfa_mtp_matches_composition(batch):
     assert np.array_equal(bits(d["hbm_kv_cache"]), hckv)
     assert np.array_equal(bits(d["hbm_k_rope"]), hkpe)
     assert_attention_close(out, gold, label="fused-mtp")
+
+
+def test_fused_copy_sfa_mtp_roles_on_separate_xcds():
+    """The MTP3 overlap kernel gives workgroups the copy or the attention role
+    by linear id, assuming workgroups are dealt to the 8 XCDs round-robin (the
+    single-partition mode), so that the copy's host reads and the attention's
+    HBM reads never share an XCD (the results do not depend on it, the speed
+    does).  Each workgroup records the XCD it ran on (hardware XCC_ID); the
+    copy role must cover 5 XCDs and the attention the other 3."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import make_chain_case
+
+    if torch.cuda.get_device_properties(0).multi_processor_count < 256:
+        pytest.skip("a partitioned device: fewer than 8 XCDs per device")
+    case = _chain_after_lim(make_chain_case(2, [4096, 6144], [2048, 2048], [4, 33], seed=3, mtp=True), mtp=True)
+    d = case.to_device("cuda")
+    _lib.xcd_roles(reset=True)
+    _run_fused(d, case.meta["scale"], mtp=True)
+    copy_xcds, attn_xcds = _lib.xcd_roles(reset=True)
+    print(f"copy XCDs {copy_xcds:#04x}, attention XCDs {attn_xcds:#04x}", flush=True)
+    assert copy_xcds & attn_xcds == 0, (hex(copy_xcds), hex(attn_xcds))
+    assert bin(copy_xcds).count("1") == 5 and bin(attn_xcds).count("1") == 3, (hex(copy_xcds), hex(attn_xcds))
+    assert _lib.xcd_roles() == (0, 0)  # the read above cleared the record
