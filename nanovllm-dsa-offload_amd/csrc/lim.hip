@@ -2113,6 +2113,114 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_kernel(const float* 
   if (tid == 0) *w.count = run;
 }
 
+// lidu_init_kernel for sources of at most NCH * kChunk tokens, with every
+// score key in registers: thread tid holds tokens k * kChunk + tid * kItems
+// + e (chunk k, e < kItems), all loaded in one round trip, and the range,
+// the radix passes and the final ordered pass all read the registers.  The
+// loads go through a buffer resource spanning the workspace's score region
+// (align256(4 row_len) bytes, a multiple of the 16-byte loads), so loads past
+// it return zeros without a branch; keys of tokens >= n are never used.
+// Same selection, slots and lists as lidu_init_kernel.
+template <int NCH>
+__global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const float* s, int n, int c,
+                                                                       int32_t* pool_row, int64_t row_len, InitWs w) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
+  // key[k][h][i]: token k * kChunk + tid * kItems + 4h + i; the loaded
+  // score bits are turned into order-preserving keys in place.
+  u32x4_t key[NCH][2];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      key[k][h] = __builtin_amdgcn_raw_buffer_load_b128(srsrc, (k * kChunk + tid * kItems + 4 * h) * 4, 0, 0);
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  // Chunks below kfull hold n's tokens only, chunk kfull is cut at n, the
+  // ones above lie past it (kfull is uniform: scalar branches, and the
+  // element checks only in the one cut chunk).
+  const int kfull = n / kChunk;
+  const int lim = n - kfull * kChunk - tid * kItems;  // element e of chunk kfull exists iff e < lim
+  auto each_key = [&](auto f) {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      if (k < kfull) {
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) f(key[k][e >> 2][e & 3]);
+      } else if (k == kfull) {
+#pragma unroll
+        for (int e = 0; e < kItems; ++e)
+          if (e < lim) f(key[k][e >> 2][e & 3]);
+      }
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) key[k][e >> 2][e & 3] = score_key(__uint_as_float(key[k][e >> 2][e & 3]));
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  each_key([&](uint32_t u) {
+    lo = min(lo, u);
+    hi = max(hi, u);
+  });
+  block_minmax(lo, hi, red);
+  const SelectOut sel = radix_select_visit(c, lo, hi, each_key, hist, scratch, bcast);
+  const bool need_rank = sel.cnt_eq != sel.need_eq;
+  int eq_run = 0, run = 0;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    if (k > kfull) continue;  // uniform: nothing selected past n (the pool row is cleared below)
+    const int64_t t0 = static_cast<int64_t>(k) * kChunk + tid * kItems;
+    unsigned selmask = 0, eqmask = 0;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      if (k == kfull && e >= lim) continue;
+      if (key[k][e >> 2][e & 3] > sel.thresh) selmask |= 1u << e;
+      if (key[k][e >> 2][e & 3] == sel.thresh) eqmask |= 1u << e;
+    }
+    if (need_rank) {
+      int tot;
+      int rk = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if ((eqmask >> e) & 1u) {
+          if (rk < sel.need_eq) selmask |= 1u << e;
+          ++rk;
+        }
+      eq_run += tot;
+    } else {
+      selmask |= eqmask;
+    }
+    int tot;
+    int pos = run + block_exclusive_scan(__popc(selmask), scratch, &tot);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      const int64_t t = t0 + e;
+      if (t >= row_len) continue;
+      if ((selmask >> e) & 1u) {
+        pool_row[t] = pos;
+        if (pos < kSlotStride) {
+          w.src[pos] = static_cast<int32_t>(t);
+          w.dst[pos] = pos;
+        }
+        ++pos;
+      } else {
+        pool_row[t] = -1;
+      }
+    }
+    run += tot;
+  }
+  // The rest of the pool row (past the chunks written above, which end at
+  // chunk min(kfull, NCH - 1)) lies past the source: nothing selected there.
+  for (int64_t t = static_cast<int64_t>(min(kfull + 1, NCH)) * kChunk + tid; t < row_len; t += kManageThreads)
+    pool_row[t] = -1;
+  if (tid == 0) *w.count = run;
+}
+
 // One workgroup: the (token, slot) list of every entry >= 0 of an owner's
 // pool row, ascending token (dsa_offload_ops.py:385-388); the count may
 // exceed the list capacity (the caller checks it).
@@ -2232,9 +2340,16 @@ hipError_t launch_lidu_init(const LiduInitArgs& a, hipStream_t stream) {
   const InitWs w = carve_init(a.workspace, a.row_len);
   hipError_t e = a.elem == Elem::kBf16 ? launch_lidu_scores<Bf16>(a, w, stream) : launch_lidu_scores<F16>(a, w, stream);
   if (e != hipSuccess) return e;
-  launch_kernel(kKernLiduInit, lidu_init_kernel, dim3(1), dim3(kManageThreads), stream,
-                static_cast<const float*>(w.scores), static_cast<int>(a.n), static_cast<int>(a.c), a.pool_row,
-                a.row_len, w);
+  const float* s = static_cast<const float*>(w.scores);
+  const int n = static_cast<int>(a.n), c = static_cast<int>(a.c);
+  // Sources of up to 32768 tokens keep their keys in registers (64 per
+  // thread; at 128 the compiler moves the array to scratch memory).
+  if (a.n <= 8 * kChunk)
+    launch_kernel(kKernLiduInit, lidu_init_reg_kernel<8>, dim3(1), dim3(kManageThreads), stream, s, n, c, a.pool_row,
+                  a.row_len, w);
+  else
+    launch_kernel(kKernLiduInit, lidu_init_kernel, dim3(1), dim3(kManageThreads), stream, s, n, c, a.pool_row,
+                  a.row_len, w);
   return hipGetLastError();
 }
 

@@ -226,6 +226,9 @@ def _oracle_init(case):
     (2, 48, 2048, 32, "bf16", False),
     (3, 72, 5000, 64, "bf16", False),
     (4, 24, 2048, 32, "f16", True),
+    (5, 256, 2048, 32, "bf16", False),   # 32768 tokens: the largest source whose keys stay in registers
+    (6, 320, 8192, 32, "bf16", True),    # 40960 tokens: the streaming kernel
+    (7, 530, 3000, 32, "bf16", False),   # 67840 tokens: the streaming kernel
 ])
 def test_gpu_initialize_lidu_row_matches_oracle(seed, n_blocks, c, heads, dtype, closed):
     from nanovllm_amd import dsa_offload_ops as ops
@@ -237,6 +240,31 @@ def test_gpu_initialize_lidu_row_matches_oracle(seed, n_blocks, c, heads, dtype,
     out = ops.initialize_lidu_row(candidate_len=case["n"], cache_tokens=c, block_size=128, **g)
     torch.cuda.synchronize()
     assert out[0] is g["hbm_kpe"] and out[1] is g["hbm_ckv"]
+    assert np.array_equal(ints(g["cache_slots_row"]), slots)
+    assert np.array_equal(bits(g["hbm_ckv"]), hckv)
+    assert np.array_equal(bits(g["hbm_kpe"]), hkpe)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_blocks", [200, 300])
+def test_gpu_initialize_lidu_row_all_ties(n_blocks):
+    """Every index key zero: every score is 0, so the C selected tokens are the
+    C lowest (ties at the threshold go to the lower tokens) and slot i goes
+    to token i; 25600 tokens (keys in registers, the last register chunk cut
+    at n) and 38400 (the streaming kernel)."""
+    from nanovllm_amd import dsa_offload_ops as ops
+
+    c = 2048
+    case = _init_case(11, n_blocks, c, 32, "bf16", closed_form=True)
+    case["keys"][:] = 0
+    print(f"LIDU-INIT all ties n={case['n']} c={c}", flush=True)
+    slots, hkpe, hckv = _oracle_init(case)
+    expect = np.full(case["slots"].shape, -1, np.int32)
+    expect[:c] = np.arange(c, dtype=np.int32)
+    assert np.array_equal(slots, expect)
+    g = _to_gpu(case)
+    ops.initialize_lidu_row(candidate_len=case["n"], cache_tokens=c, block_size=128, **g)
+    torch.cuda.synchronize()
     assert np.array_equal(ints(g["cache_slots_row"]), slots)
     assert np.array_equal(bits(g["hbm_ckv"]), hckv)
     assert np.array_equal(bits(g["hbm_kpe"]), hkpe)
