@@ -2128,6 +2128,7 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const flo
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
+  __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
@@ -2169,55 +2170,81 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const flo
   });
   block_minmax(lo, hi, red);
   const SelectOut sel = radix_select_visit(c, lo, hi, each_key, hist, scratch, bcast);
-  const bool need_rank = sel.cnt_eq != sel.need_eq;
-  int eq_run = 0, run = 0;
+  // The ordered pass: this thread's selection and tie masks in every chunk,
+  // then one 8-counter block scan (two with ties to rank) gives every
+  // chunk's slot positions at once (a chunk holds 4096 tokens, below the
+  // scan's 16-bit counters).  Token order is chunk-major, so the tokens
+  // before this thread's chunk-k ones are the earlier chunks' totals plus
+  // the chunk-k counts of the lower threads.
+  unsigned selm[NCH], eqm[NCH];
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
-    if (k > kfull) continue;  // uniform: nothing selected past n (the pool row is cleared below)
-    const int64_t t0 = static_cast<int64_t>(k) * kChunk + tid * kItems;
-    unsigned selmask = 0, eqmask = 0;
+    selm[k] = 0u;
+    eqm[k] = 0u;
+    if (k > kfull) continue;  // uniform
 #pragma unroll
     for (int e = 0; e < kItems; ++e) {
       if (k == kfull && e >= lim) continue;
-      if (key[k][e >> 2][e & 3] > sel.thresh) selmask |= 1u << e;
-      if (key[k][e >> 2][e & 3] == sel.thresh) eqmask |= 1u << e;
+      if (key[k][e >> 2][e & 3] > sel.thresh) selm[k] |= 1u << e;
+      if (key[k][e >> 2][e & 3] == sel.thresh) eqm[k] |= 1u << e;
     }
-    if (need_rank) {
-      int tot;
-      int rk = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
+  }
+  if (sel.cnt_eq != sel.need_eq) {  // only the lowest need_eq tied tokens are selected
+    uint64_t ec[2] = {0, 0}, etot[2];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) ec[k >> 2] |= static_cast<uint64_t>(__popc(eqm[k])) << (16 * (k & 3));
+    block_exclusive_scan8(ec, scan64, etot);
+    int ebase = 0;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      int rk = ebase + lane16x8(ec, k);
 #pragma unroll
       for (int e = 0; e < kItems; ++e)
-        if ((eqmask >> e) & 1u) {
-          if (rk < sel.need_eq) selmask |= 1u << e;
+        if ((eqm[k] >> e) & 1u) {
+          if (rk < sel.need_eq) selm[k] |= 1u << e;
           ++rk;
         }
-      eq_run += tot;
-    } else {
-      selmask |= eqmask;
+      ebase += lane16x8(etot, k);
     }
-    int tot;
-    int pos = run + block_exclusive_scan(__popc(selmask), scratch, &tot);
+  } else {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) selm[k] |= eqm[k];
+  }
+  uint64_t sc[2] = {0, 0}, stot[2];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) sc[k >> 2] |= static_cast<uint64_t>(__popc(selm[k])) << (16 * (k & 3));
+  block_exclusive_scan8(sc, scan64, stot);
+  const bool vec_ok = (reinterpret_cast<uintptr_t>(pool_row) & 15) == 0;  // uniform
+  int run = 0;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int64_t t0 = static_cast<int64_t>(k) * kChunk + tid * kItems;
+    int pos = run + lane16x8(sc, k);
+    int pv[kItems];
 #pragma unroll
     for (int e = 0; e < kItems; ++e) {
-      const int64_t t = t0 + e;
-      if (t >= row_len) continue;
-      if ((selmask >> e) & 1u) {
-        pool_row[t] = pos;
+      pv[e] = -1;
+      if ((selm[k] >> e) & 1u) {
+        pv[e] = pos;
         if (pos < kSlotStride) {
-          w.src[pos] = static_cast<int32_t>(t);
+          w.src[pos] = static_cast<int32_t>(t0 + e);
           w.dst[pos] = pos;
         }
         ++pos;
-      } else {
-        pool_row[t] = -1;
       }
     }
-    run += tot;
+    if (vec_ok && t0 + kItems <= row_len) {
+      *reinterpret_cast<int4*>(pool_row + t0) = make_int4(pv[0], pv[1], pv[2], pv[3]);
+      *reinterpret_cast<int4*>(pool_row + t0 + 4) = make_int4(pv[4], pv[5], pv[6], pv[7]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (t0 + e < row_len) pool_row[t0 + e] = pv[e];
+    }
+    run += lane16x8(stot, k);
   }
-  // The rest of the pool row (past the chunks written above, which end at
-  // chunk min(kfull, NCH - 1)) lies past the source: nothing selected there.
-  for (int64_t t = static_cast<int64_t>(min(kfull + 1, NCH)) * kChunk + tid; t < row_len; t += kManageThreads)
-    pool_row[t] = -1;
+  // The rest of the pool row lies past the source: nothing selected there.
+  for (int64_t t = static_cast<int64_t>(NCH) * kChunk + tid; t < row_len; t += kManageThreads) pool_row[t] = -1;
   if (tid == 0) *w.count = run;
 }
 
