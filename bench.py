@@ -968,6 +968,19 @@ def measure_lidu_init(torch, np, dev, seed: int, reps: int = 5):
         km = _kernel_means(kt, ("lim_score_kernel", "lidu_init_kernel", "scatter_copy_kernel"))
         out[f"C{c}"] = {"kernels_us": km, "copy_h2d_GBs": round(c * ROW_BYTES / (km["scatter_copy_kernel"] * 1e-6)
                                                                  / 1e9, 2)}
+    # A shared layer's copy of the owner's C = 8192 mapping, the pool row as
+    # wide as the model runner's (65536 entries).
+    row64 = torch.full((65536,), -1, dtype=torch.int32, device=dev)
+    row64[:n] = row
+    skw = dict(cache_slots_row=row64, cache_tokens=8192, hbm_kpe=hkpe, hbm_ckv=hckv, dram_kpe=dkpe, dram_ckv=dckv,
+               hbm_block_table=htab, dram_block_table=table)
+    ops.initialize_lidu_row_shared(**skw)
+    torch.cuda.synchronize()
+    with _lib.KernelTimer(capacity=4 * reps) as kt:
+        for _ in range(reps):
+            ops.initialize_lidu_row_shared(**skw)
+        torch.cuda.synchronize()
+    out["shared_C8192_row65536"] = {"kernels_us": _kernel_means(kt, ("lidu_shared_kernel", "scatter_copy_kernel"))}
     del keys, dkpe, dckv
     torch.cuda.empty_cache()
     return out

@@ -2253,30 +2253,56 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const flo
 // exceed the list capacity (the caller checks it).
 __global__ __launch_bounds__(kManageThreads) void lidu_shared_kernel(const int32_t* pool_row, int64_t row_len,
                                                                      InitWs w) {
-  __shared__ int scratch[kManageThreads / 64 + 1];
+  // Groups of 8 chunks of 4096 entries: thread tid reads entries
+  // k * kChunk + tid * kItems + e of each chunk k of the group (16-byte loads
+  // when the row is 16-byte aligned), all in flight together, and one block
+  // scan of eight 16-bit counters orders the group's cached tokens.
+  __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
+  constexpr int kGroup = 8;
   const int tid = threadIdx.x;
+  const bool vec_ok = (reinterpret_cast<uintptr_t>(pool_row) & 15) == 0;  // uniform
   int run = 0;
-  for (int64_t base = 0; base < row_len; base += kChunk) {
-    const int64_t t0 = base + static_cast<int64_t>(tid) * kItems;
-    int32_t v[kItems];
-    unsigned mask = 0;
+  for (int64_t gbase = 0; gbase < row_len; gbase += kGroup * kChunk) {
+    int32_t v[kGroup][kItems];
 #pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      v[e] = t0 + e < row_len ? pool_row[t0 + e] : -1;
-      if (v[e] >= 0) mask |= 1u << e;
-    }
-    int tot;
-    int pos = run + block_exclusive_scan(__popc(mask), scratch, &tot);
+    for (int k = 0; k < kGroup; ++k) {
+      const int64_t t0 = gbase + static_cast<int64_t>(k) * kChunk + tid * kItems;
+      if (vec_ok && t0 + kItems <= row_len) {
+        const int4 x = *reinterpret_cast<const int4*>(pool_row + t0);
+        const int4 y = *reinterpret_cast<const int4*>(pool_row + t0 + 4);
+        v[k][0] = x.x; v[k][1] = x.y; v[k][2] = x.z; v[k][3] = x.w;
+        v[k][4] = y.x; v[k][5] = y.y; v[k][6] = y.z; v[k][7] = y.w;
+      } else {
 #pragma unroll
-    for (int e = 0; e < kItems; ++e)
-      if ((mask >> e) & 1u) {
-        if (pos < kSlotStride) {
-          w.src[pos] = static_cast<int32_t>(t0 + e);
-          w.dst[pos] = v[e];
-        }
-        ++pos;
+        for (int e = 0; e < kItems; ++e) v[k][e] = t0 + e < row_len ? pool_row[t0 + e] : -1;
       }
-    run += tot;
+    }
+    uint64_t cnt[2] = {0, 0}, tot[2];
+    unsigned mask[kGroup];
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      mask[k] = 0u;
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (v[k][e] >= 0) mask[k] |= 1u << e;
+      cnt[k >> 2] |= static_cast<uint64_t>(__popc(mask[k])) << (16 * (k & 3));
+    }
+    block_exclusive_scan8(cnt, scan64, tot);
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const int64_t t0 = gbase + static_cast<int64_t>(k) * kChunk + tid * kItems;
+      int pos = run + lane16x8(cnt, k);
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if ((mask[k] >> e) & 1u) {
+          if (pos < kSlotStride) {
+            w.src[pos] = static_cast<int32_t>(t0 + e);
+            w.dst[pos] = v[k][e];
+          }
+          ++pos;
+        }
+      run += lane16x8(tot, k);
+    }
   }
   if (tid == 0) *w.count = run;
 }

@@ -245,6 +245,61 @@ def test_gpu_initialize_lidu_row_matches_oracle(seed, n_blocks, c, heads, dtype,
     assert np.array_equal(bits(g["hbm_kpe"]), hkpe)
 
 
+def _unaligned(t: torch.Tensor) -> torch.Tensor:
+    """A copy of 1-D ``t`` whose data starts 4 bytes into an allocation (not
+    16-byte aligned), so the kernels take their element-wise path."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    view = buf[1:]
+    view.copy_(t)
+    assert view.data_ptr() % 16 != 0
+    return view
+
+
+@pytest.mark.gpu
+def test_gpu_initialize_lidu_row_unaligned_pool_row():
+    """32768 candidates (keys in registers) written into a pool row that is
+    not 16-byte aligned."""
+    from nanovllm_amd import dsa_offload_ops as ops
+
+    case = _init_case(5, 256, 2048, 32, "bf16", False)
+    print(f"LIDU-INIT unaligned row n={case['n']}", flush=True)
+    slots, hkpe, hckv = _oracle_init(case)
+    g = _to_gpu(case)
+    g["cache_slots_row"] = _unaligned(g["cache_slots_row"])
+    ops.initialize_lidu_row(candidate_len=case["n"], cache_tokens=2048, block_size=128, **g)
+    torch.cuda.synchronize()
+    assert np.array_equal(ints(g["cache_slots_row"]), slots)
+    assert np.array_equal(bits(g["hbm_ckv"]), hckv)
+    assert np.array_equal(bits(g["hbm_kpe"]), hkpe)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("aligned", [True, False])
+def test_gpu_initialize_lidu_row_shared_long_row(aligned):
+    """An owner pool row of 67840 entries (groups of 8 x 4096 entries, the
+    last one partial) with 5000 cached tokens spread over it, 16-byte
+    aligned or not: the shared layer copies exactly the owner's mapping."""
+    from nanovllm_amd import dsa_offload_ops as ops
+
+    c = 5000
+    case = _init_case(12, 530, c, closed_form=True)
+    rng = np.random.default_rng(13)
+    slots = np.full(case["slots"].shape, -1, np.int32)
+    slots[rng.choice(case["n"], c, replace=False)] = rng.permutation(c).astype(np.int32)
+    hkpe, hckv = case["hkpe"].copy(), case["hckv"].copy()
+    O.initialize_lidu_row_shared(slots, c, hkpe, hckv, case["dkpe"], case["dckv"], case["htab"], case["dtab"])
+    print(f"LIDU-SHARED row {slots.shape[0]} entries, {c} cached, aligned={aligned}", flush=True)
+    g = _to_gpu(dict(case, slots=slots))
+    row = g["cache_slots_row"] if aligned else _unaligned(g["cache_slots_row"])
+    ops.initialize_lidu_row_shared(cache_slots_row=row, cache_tokens=c, hbm_kpe=g["hbm_kpe"], hbm_ckv=g["hbm_ckv"],
+                                   dram_kpe=g["dram_kpe"], dram_ckv=g["dram_ckv"],
+                                   hbm_block_table=g["hbm_block_table"], dram_block_table=g["dram_block_table"])
+    torch.cuda.synchronize()
+    assert np.array_equal(ints(row), slots)  # the owner's row is read, not written
+    assert np.array_equal(bits(g["hbm_ckv"]), hckv)
+    assert np.array_equal(bits(g["hbm_kpe"]), hkpe)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("n_blocks", [200, 300])
 def test_gpu_initialize_lidu_row_all_ties(n_blocks):
