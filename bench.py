@@ -981,7 +981,24 @@ def measure_lidu_init(torch, np, dev, seed: int, reps: int = 5):
             ops.initialize_lidu_row_shared(**skw)
         torch.cuda.synchronize()
     out["shared_C8192_row65536"] = {"kernels_us": _kernel_means(kt, ("lidu_shared_kernel", "scatter_copy_kernel"))}
-    del keys, dkpe, dckv
+    # A 65536-token source (C = 2048): the selection streams the scores in
+    # groups of 32768 tokens per pass.
+    n64, nb64 = 65536, 512
+    keys64 = torch.randn(nb64, 128, 1, 128, generator=g).to(torch.bfloat16).to(dev)
+    table64 = torch.randperm(nb64, generator=g).to(torch.int32).to(dev)
+    dkpe64 = empty_host_mapped((nb64, 128, 64), torch.bfloat16, dev)
+    dckv64 = empty_host_mapped((nb64, 128, 512), torch.bfloat16, dev)
+    kw = dict(query=q, weights=w, index_cache=keys64, index_block_table=table64, candidate_len=n64, cache_tokens=2048,
+              cache_slots_row=row64, hbm_kpe=hkpe, hbm_ckv=hckv, dram_kpe=dkpe64, dram_ckv=dckv64,
+              hbm_block_table=htab, dram_block_table=table64, block_size=128)
+    ops.initialize_lidu_row(**kw)
+    torch.cuda.synchronize()
+    with _lib.KernelTimer(capacity=8 * reps) as kt:
+        for _ in range(reps):
+            ops.initialize_lidu_row(**kw)
+        torch.cuda.synchronize()
+    out["n65536_C2048"] = {"kernels_us": _kernel_means(kt, ("lim_score_kernel", "lidu_init_kernel"))}
+    del keys, dkpe, dckv, keys64, dkpe64, dckv64
     torch.cuda.empty_cache()
     return out
 

@@ -331,7 +331,7 @@ struct SelectOut {
 // thread reads the wave results itself).  LDS_ONLY: barriers that order LDS
 // only.
 template <bool LDS_ONLY = false>
-__device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
+__device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
     lo = min(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), d, 64)));
@@ -367,7 +367,8 @@ __device__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
 // Requires (#included) >= k >= 1.  `hist` must be zero on entry and is zero
 // again on return (each owner clears its bins after reading them).
 template <typename Visit>
-__device__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Visit visit, uint32_t* hist,
+__device__ __forceinline__ SelectOut radix_select_visit(int k, uint32_t kmin, uint32_t kmax, Visit visit,
+                                                        uint32_t* hist,
                                         int* scratch, int* bcast) {
   if (kmax == kmin) return SelectOut{kmin, k, INT_MAX};
   const int tid = threadIdx.x;
@@ -2036,149 +2037,86 @@ InitWs carve_init(void* base, int64_t cap) {
   return w;
 }
 
-// One workgroup: the C largest linear scores of tokens [0, n) (ties at the
-// threshold to the lower tokens), slot i to the i-th smallest selected token,
-// the pool row rewritten over its whole length (-1 outside the selection),
-// and the (token, slot) copy list.
-__global__ __launch_bounds__(kManageThreads) void lidu_init_kernel(const float* s, int n, int c, int32_t* pool_row,
-                                                                   int64_t row_len, InitWs w) {
-  __shared__ uint32_t hist[kBins];
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
-  __shared__ int bcast[4];
-  const int tid = threadIdx.x;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  const int ngroups = static_cast<int>(ceil_div(n, 4));
-  uint32_t lo = 0xffffffffu, hi = 0u;
-  for (int g = tid; g < ngroups; g += kManageThreads) {
-    uint32_t key[4];
-    bool inc[4];
-    load_score_keys(s, n, 4 * g, key, inc);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (inc[e]) {
-        lo = min(lo, key[e]);
-        hi = max(hi, key[e]);
-      }
-  }
-  block_minmax(lo, hi, red);
-  const SelectOut sel = radix_select(
-      ngroups, c, lo, hi, [&](int g, uint32_t* key, bool* inc) { load_score_keys(s, n, 4 * g, key, inc); }, hist,
-      scratch, bcast);
-  const bool need_rank = sel.cnt_eq != sel.need_eq;
-  int eq_run = 0, run = 0;
-  for (int64_t base = 0; base < row_len; base += kChunk) {
-    const int64_t t0 = base + static_cast<int64_t>(tid) * kItems;
-    unsigned selmask = 0, eqmask = 0;
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      const int64_t t = t0 + e;
-      if (t >= n) continue;
-      const uint32_t u = score_key(s[t]);
-      if (u > sel.thresh) selmask |= 1u << e;
-      if (u == sel.thresh) eqmask |= 1u << e;
-    }
-    if (need_rank) {
-      int tot;
-      int rk = eq_run + block_exclusive_scan(__popc(eqmask), scratch, &tot);
-#pragma unroll
-      for (int e = 0; e < kItems; ++e)
-        if ((eqmask >> e) & 1u) {
-          if (rk < sel.need_eq) selmask |= 1u << e;
-          ++rk;
-        }
-      eq_run += tot;
-    } else {
-      selmask |= eqmask;
-    }
-    int tot;
-    int pos = run + block_exclusive_scan(__popc(selmask), scratch, &tot);
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      const int64_t t = t0 + e;
-      if (t >= row_len) continue;
-      if ((selmask >> e) & 1u) {
-        pool_row[t] = pos;
-        if (pos < kSlotStride) {
-          w.src[pos] = static_cast<int32_t>(t);
-          w.dst[pos] = pos;
-        }
-        ++pos;
-      } else {
-        pool_row[t] = -1;
-      }
-    }
-    run += tot;
-  }
-  if (tid == 0) *w.count = run;
-}
+// Tokens per group of the first-decode selection: 8 chunks of kChunk, thread
+// tid holding tokens gbase + k * kChunk + tid * kItems + e of group gbase.
+constexpr int kInitGroup = 8;
 
-// lidu_init_kernel for sources of at most NCH * kChunk tokens, with every
-// score key in registers: thread tid holds tokens k * kChunk + tid * kItems
-// + e (chunk k, e < kItems), all loaded in one round trip, and the range,
-// the radix passes and the final ordered pass all read the registers.  The
-// loads go through a buffer resource spanning the workspace's score region
-// (align256(4 row_len) bytes, a multiple of the 16-byte loads), so loads past
-// it return zeros without a branch; keys of tokens >= n are never used.
-// Same selection, slots and lists as lidu_init_kernel.
-template <int NCH>
-__global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const float* s, int n, int c,
-                                                                       int32_t* pool_row, int64_t row_len, InitWs w) {
-  __shared__ uint32_t hist[kBins];
-  __shared__ int scratch[kManageThreads / 64 + 1];
-  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
-  __shared__ int bcast[4];
-  __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
-  const int tid = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
-  // key[k][h][i]: token k * kChunk + tid * kItems + 4h + i; the loaded
-  // score bits are turned into order-preserving keys in place.
-  u32x4_t key[NCH][2];
+// One group's score keys: 16 loads per thread in flight together, through a
+// buffer resource over the workspace's score region (align256(4 row_len)
+// bytes, a multiple of the 16-byte loads, so loads past it return zeros
+// without a branch; keys of tokens >= n are never used), turned into
+// order-preserving keys in place.
+__device__ __forceinline__ void load_init_group(__amdgpu_buffer_rsrc_t rsrc, int64_t gbase,
+                                                u32x4_t (&key)[kInitGroup][2]) {
 #pragma unroll
-  for (int k = 0; k < NCH; ++k)
+  for (int k = 0; k < kInitGroup; ++k)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-      key[k][h] = __builtin_amdgcn_raw_buffer_load_b128(srsrc, (k * kChunk + tid * kItems + 4 * h) * 4, 0, 0);
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
-  // Chunks below kfull hold n's tokens only, chunk kfull is cut at n, the
-  // ones above lie past it (kfull is uniform: scalar branches, and the
-  // element checks only in the one cut chunk).
-  const int kfull = n / kChunk;
-  const int lim = n - kfull * kChunk - tid * kItems;  // element e of chunk kfull exists iff e < lim
-  auto each_key = [&](auto f) {
+      key[k][h] = __builtin_amdgcn_raw_buffer_load_b128(
+          rsrc, static_cast<int>((gbase + k * kChunk + threadIdx.x * kItems + 4 * h) * 4), 0, 0);
 #pragma unroll
-    for (int k = 0; k < NCH; ++k) {
-      if (k < kfull) {
-#pragma unroll
-        for (int e = 0; e < kItems; ++e) f(key[k][e >> 2][e & 3]);
-      } else if (k == kfull) {
-#pragma unroll
-        for (int e = 0; e < kItems; ++e)
-          if (e < lim) f(key[k][e >> 2][e & 3]);
-      }
-    }
-  };
-#pragma unroll
-  for (int k = 0; k < NCH; ++k)
+  for (int k = 0; k < kInitGroup; ++k)
 #pragma unroll
     for (int e = 0; e < kItems; ++e) key[k][e >> 2][e & 3] = score_key(__uint_as_float(key[k][e >> 2][e & 3]));
-  uint32_t lo = 0xffffffffu, hi = 0u;
-  each_key([&](uint32_t u) {
-    lo = min(lo, u);
-    hi = max(hi, u);
-  });
-  block_minmax(lo, hi, red);
-  const SelectOut sel = radix_select_visit(c, lo, hi, each_key, hist, scratch, bcast);
-  // The ordered pass: this thread's selection and tie masks in every chunk,
-  // then one 8-counter block scan (two with ties to rank) gives every
-  // chunk's slot positions at once (a chunk holds 4096 tokens, below the
-  // scan's 16-bit counters).  Token order is chunk-major, so the tokens
-  // before this thread's chunk-k ones are the earlier chunks' totals plus
-  // the chunk-k counts of the lower threads.
-  unsigned selm[NCH], eqm[NCH];
+}
+
+// f(key) for every key of tokens < n in a group: chunks below kfull are
+// whole, chunk kfull is cut at n (element e exists iff e < lim), the ones
+// above lie past n; kfull is uniform, so the element checks stay in the one
+// cut chunk.
+template <typename F>
+__device__ __forceinline__ void visit_init_group(const u32x4_t (&key)[kInitGroup][2], int kfull, int lim, const F& f) {
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) {
+  for (int k = 0; k < kInitGroup; ++k) {
+    if (k < kfull) {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) f(key[k][e >> 2][e & 3]);
+    } else if (k == kfull) {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (e < lim) f(key[k][e >> 2][e & 3]);
+    }
+  }
+}
+
+// Smallest and largest key of the group's tokens < n (kfull, lim as for
+// visit_init_group), folded into lo and hi.
+__device__ __forceinline__ void group_minmax(const u32x4_t (&key)[kInitGroup][2], int kfull, int lim, uint32_t& lo,
+                                             uint32_t& hi) {
+#pragma unroll
+  for (int k = 0; k < kInitGroup; ++k) {
+    if (k < kfull) {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e) {
+        lo = min(lo, key[k][e >> 2][e & 3]);
+        hi = max(hi, key[k][e >> 2][e & 3]);
+      }
+    } else if (k == kfull) {
+#pragma unroll
+      for (int e = 0; e < kItems; ++e)
+        if (e < lim) {
+          lo = min(lo, key[k][e >> 2][e & 3]);
+          hi = max(hi, key[k][e >> 2][e & 3]);
+        }
+    }
+  }
+}
+
+// The ordered pass over one group: slot positions of its selected tokens
+// from one 8-counter block scan (two when tied keys must be ranked: only the
+// lowest need_eq tokens equal to the threshold are selected; `eq_run` counts
+// the ties of earlier groups), the pool entries (-1 elsewhere; 16-byte stores
+// when the row allows) and the copy list.  Token order is chunk-major, so the
+// tokens before this thread's chunk-k ones are the earlier chunks' totals
+// plus the chunk-k counts of the lower threads.  Returns the group's count.
+__device__ __forceinline__ int init_group_order(const u32x4_t (&key)[kInitGroup][2], int kfull, int lim,
+                                                const SelectOut& sel, int64_t gbase, int run, int& eq_run,
+                                                int32_t* pool_row, int64_t row_len, bool vec_ok, const InitWs& w,
+                                                uint64_t* scan64) {
+  const int tid = threadIdx.x;
+  unsigned selm[kInitGroup], eqm[kInitGroup];
+#pragma unroll
+  for (int k = 0; k < kInitGroup; ++k) {
     selm[k] = 0u;
     eqm[k] = 0u;
     if (k > kfull) continue;  // uniform
@@ -2189,37 +2127,35 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const flo
       if (key[k][e >> 2][e & 3] == sel.thresh) eqm[k] |= 1u << e;
     }
   }
-  if (sel.cnt_eq != sel.need_eq) {  // only the lowest need_eq tied tokens are selected
+  if (sel.cnt_eq != sel.need_eq) {
     uint64_t ec[2] = {0, 0}, etot[2];
 #pragma unroll
-    for (int k = 0; k < NCH; ++k) ec[k >> 2] |= static_cast<uint64_t>(__popc(eqm[k])) << (16 * (k & 3));
+    for (int k = 0; k < kInitGroup; ++k) ec[k >> 2] |= static_cast<uint64_t>(__popc(eqm[k])) << (16 * (k & 3));
     block_exclusive_scan8(ec, scan64, etot);
-    int ebase = 0;
 #pragma unroll
-    for (int k = 0; k < NCH; ++k) {
-      int rk = ebase + lane16x8(ec, k);
+    for (int k = 0; k < kInitGroup; ++k) {
+      int rk = eq_run + lane16x8(ec, k);
 #pragma unroll
       for (int e = 0; e < kItems; ++e)
         if ((eqm[k] >> e) & 1u) {
           if (rk < sel.need_eq) selm[k] |= 1u << e;
           ++rk;
         }
-      ebase += lane16x8(etot, k);
+      eq_run += lane16x8(etot, k);
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < NCH; ++k) selm[k] |= eqm[k];
+    for (int k = 0; k < kInitGroup; ++k) selm[k] |= eqm[k];
   }
   uint64_t sc[2] = {0, 0}, stot[2];
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) sc[k >> 2] |= static_cast<uint64_t>(__popc(selm[k])) << (16 * (k & 3));
+  for (int k = 0; k < kInitGroup; ++k) sc[k >> 2] |= static_cast<uint64_t>(__popc(selm[k])) << (16 * (k & 3));
   block_exclusive_scan8(sc, scan64, stot);
-  const bool vec_ok = (reinterpret_cast<uintptr_t>(pool_row) & 15) == 0;  // uniform
-  int run = 0;
+  int count = 0;
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) {
-    const int64_t t0 = static_cast<int64_t>(k) * kChunk + tid * kItems;
-    int pos = run + lane16x8(sc, k);
+  for (int k = 0; k < kInitGroup; ++k) {
+    const int64_t t0 = gbase + static_cast<int64_t>(k) * kChunk + tid * kItems;
+    int pos = run + count + lane16x8(sc, k);
     int pv[kItems];
 #pragma unroll
     for (int e = 0; e < kItems; ++e) {
@@ -2241,10 +2177,92 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const flo
       for (int e = 0; e < kItems; ++e)
         if (t0 + e < row_len) pool_row[t0 + e] = pv[e];
     }
-    run += lane16x8(stot, k);
+    count += lane16x8(stot, k);
   }
+  return count;
+}
+
+// One workgroup: the C largest linear scores of tokens [0, n) (ties at the
+// threshold to the lower tokens), slot i to the i-th smallest selected token,
+// the pool row rewritten over its whole length (-1 outside the selection),
+// and the (token, slot) copy list.  Any n: every pass (range, radix digits,
+// ordered pass) walks the scores group by group, one load round trip per
+// group of 32768 tokens.
+__global__ __launch_bounds__(kManageThreads) void lidu_init_kernel(const float* s, int n, int c, int32_t* pool_row,
+                                                                   int64_t row_len, InitWs w) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  constexpr int kGroupTokens = kInitGroup * kChunk;
+  auto each_key = [&](auto f) {
+    for (int gbase = 0; gbase < n; gbase += kGroupTokens) {
+      u32x4_t key[kInitGroup][2];
+      load_init_group(srsrc, gbase, key);
+      const int kfull = (n - gbase) / kChunk;
+      visit_init_group(key, kfull, n - gbase - kfull * kChunk - tid * kItems, f);
+    }
+  };
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int gbase = 0; gbase < n; gbase += kGroupTokens) {
+    u32x4_t key[kInitGroup][2];
+    load_init_group(srsrc, gbase, key);
+    const int kfull = (n - gbase) / kChunk;
+    group_minmax(key, kfull, n - gbase - kfull * kChunk - tid * kItems, lo, hi);
+  }
+  block_minmax(lo, hi, red);
+  const SelectOut sel = radix_select_visit(c, lo, hi, each_key, hist, scratch, bcast);
+  const bool vec_ok = (reinterpret_cast<uintptr_t>(pool_row) & 15) == 0;  // uniform
+  int run = 0, eq_run = 0;
+  for (int64_t gbase = 0; gbase < row_len; gbase += kGroupTokens) {
+    if (gbase >= n) {  // past the source: nothing selected
+      for (int64_t t = gbase + tid; t < min<int64_t>(row_len, gbase + kGroupTokens); t += kManageThreads)
+        pool_row[t] = -1;
+      continue;
+    }
+    u32x4_t key[kInitGroup][2];
+    load_init_group(srsrc, gbase, key);
+    const int kfull = static_cast<int>((n - gbase) / kChunk);
+    run += init_group_order(key, kfull, static_cast<int>(n - gbase - kfull * kChunk - tid * kItems), sel, gbase, run,
+                            eq_run, pool_row, row_len, vec_ok, w, scan64);
+  }
+  if (tid == 0) *w.count = run;
+}
+
+// lidu_init_kernel for sources of at most one group (32768 tokens): the
+// group's keys stay in registers across the range, the radix passes and the
+// ordered pass instead of being re-read for each.
+__global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const float* s, int n, int c,
+                                                                       int32_t* pool_row, int64_t row_len, InitWs w) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ int scratch[kManageThreads / 64 + 1];
+  __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
+  __shared__ int bcast[4];
+  __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
+  u32x4_t key[kInitGroup][2];
+  load_init_group(srsrc, 0, key);
+  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  const int kfull = n / kChunk;
+  const int lim = n - kfull * kChunk - tid * kItems;
+  auto each_key = [&](auto f) { visit_init_group(key, kfull, lim, f); };
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  group_minmax(key, kfull, lim, lo, hi);
+  block_minmax(lo, hi, red);
+  const SelectOut sel = radix_select_visit(c, lo, hi, each_key, hist, scratch, bcast);
+  int eq_run = 0;
+  const int run = init_group_order(key, kfull, lim, sel, 0, 0, eq_run, pool_row, row_len,
+                                   (reinterpret_cast<uintptr_t>(pool_row) & 15) == 0, w, scan64);
   // The rest of the pool row lies past the source: nothing selected there.
-  for (int64_t t = static_cast<int64_t>(NCH) * kChunk + tid; t < row_len; t += kManageThreads) pool_row[t] = -1;
+  for (int64_t t = static_cast<int64_t>(kInitGroup) * kChunk + tid; t < row_len; t += kManageThreads)
+    pool_row[t] = -1;
   if (tid == 0) *w.count = run;
 }
 
@@ -2395,10 +2413,10 @@ hipError_t launch_lidu_init(const LiduInitArgs& a, hipStream_t stream) {
   if (e != hipSuccess) return e;
   const float* s = static_cast<const float*>(w.scores);
   const int n = static_cast<int>(a.n), c = static_cast<int>(a.c);
-  // Sources of up to 32768 tokens keep their keys in registers (64 per
-  // thread; at 128 the compiler moves the array to scratch memory).
-  if (a.n <= 8 * kChunk)
-    launch_kernel(kKernLiduInit, lidu_init_reg_kernel<8>, dim3(1), dim3(kManageThreads), stream, s, n, c, a.pool_row,
+  // Sources of up to one group (32768 tokens) keep their keys in registers
+  // (64 per thread; at 128 the compiler moved the array to scratch memory).
+  if (a.n <= kInitGroup * kChunk)
+    launch_kernel(kKernLiduInit, lidu_init_reg_kernel, dim3(1), dim3(kManageThreads), stream, s, n, c, a.pool_row,
                   a.row_len, w);
   else
     launch_kernel(kKernLiduInit, lidu_init_kernel, dim3(1), dim3(kManageThreads), stream, s, n, c, a.pool_row,
