@@ -2041,6 +2041,13 @@ InitWs carve_init(void* base, int64_t cap) {
 // tid holding tokens gbase + k * kChunk + tid * kItems + e of group gbase.
 constexpr int kInitGroup = 8;
 
+// Byte range of the buffer resource over the score region: align256(4 row_len)
+// (a multiple of the 16-byte loads), capped at 1 GiB so it fits the 32-bit
+// field; every load offset stays below 4 (n + one group) < 9 MB (n < 2^21).
+__device__ inline int init_score_range(int64_t row_len) {
+  return static_cast<int>(min<size_t>(align256(sizeof(float) * row_len), size_t(1) << 30));
+}
+
 // One group's score keys: 16 loads per thread in flight together, through a
 // buffer resource over the workspace's score region (align256(4 row_len)
 // bytes, a multiple of the 16-byte loads, so loads past it return zeros
@@ -2196,8 +2203,8 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_kernel(const float* 
   __shared__ int bcast[4];
   __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
   const int tid = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t srsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(s), 0, init_score_range(row_len), kBufferFlags);
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
   constexpr int kGroupTokens = kInitGroup * kChunk;
   auto each_key = [&](auto f) {
@@ -2245,8 +2252,8 @@ __global__ __launch_bounds__(kManageThreads) void lidu_init_reg_kernel(const flo
   __shared__ int bcast[4];
   __shared__ uint64_t scan64[2 * (kManageThreads / 64)];
   const int tid = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(s), 0, static_cast<int>(align256(sizeof(float) * row_len)), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t srsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(s), 0, init_score_range(row_len), kBufferFlags);
   u32x4_t key[kInitGroup][2];
   load_init_group(srsrc, 0, key);
   for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
