@@ -671,11 +671,13 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
                                t["hbm_block_table"], t["dram_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"],
                                t["dram_k_rope"], t["dram_kv_cache"], case.meta["scale"], t["attention_out"])
 
-    _lib.xcd_roles(reset=True)
-    for _ in range(2):
+    for i in range(2):
         t["cache_slots_pool"].copy_(pool0)
+        if i == 1:
+            _lib.xcd_roles(reset=True)
         step()
-    # the XCDs the overlap kernel's copy and attention workgroups ran on in the two warm-up steps
+    # the XCDs the overlap kernel's copy and attention workgroups ran on in the second warm-up step
+    # (one launch: the dispatcher's starting XCD may differ between launches)
     copy_xcds, attn_xcds = _lib.xcd_roles(reset=True)
     times = []
     with _lib.KernelTimer(capacity=16 * reps) as kt:

@@ -126,9 +126,9 @@ Partials carve(void* ws, int64_t rows, int64_t splits, int64_t heads) {
   return p;
 }
 
-// MTP3 overlap launch: XCDs [0, kCopyXcds) copy (one XCD pulls ~13 GB/s
-// from host memory), the others attend; 32 CUs per XCD, one resident
-// workgroup per CU.
+// MTP3 overlap launch: the workgroups on kCopyXcds of the 8 XCDs copy (one
+// XCD pulls ~13 GB/s from host memory), the others attend; 32 CUs per XCD,
+// one resident workgroup per CU.
 constexpr int kCopyXcds = 5;
 constexpr int kCopyWgs = kCopyXcds * 32;
 
@@ -593,8 +593,9 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 // MTP3 fused_copy_sfa, first launch: attention over the HBM-resident keys
 // (kKeysResident) and the DRAM -> HBM copy of the union misses, side by side
 // on separate XCDs.  Workgroups are dealt to the 8 XCDs round-robin by
-// linear id; those on XCDs [0, kCopyXcds) copy (a grid-stride loop over
-// 16-row chunks of every request), the rest attend.  Host reads in flight
+// linear id (from a starting XCD that can differ between dispatches), so
+// those with id mod 8 < kCopyXcds share 5 XCDs: they copy (a grid-stride
+// loop over 16-row chunks of every request), the rest attend.  Host reads in flight
 // stall HBM reads issued on the same XCD, so the two roles do not share one.
 // No workgroup waits on another: the copied keys are attended by a second
 // launch on the same stream.
