@@ -10,17 +10,21 @@ out: block tables padded to ceil(max_model_len/128) = 512 columns and a
 65536-wide slot pool.  The index query alternates between two calibrated
 queries whose top-2048 sets differ by each request's target miss fraction,
 so every step really misses and copies ~5-15% of its selection and no state
-is restored inside the timed region.  Steps are replayed from captured HIP
-graphs (the serving path; the reference times graph replays too), two
-consecutive layer-steps per graph replay (the serving graph spans every
-layer of a decode step, so its launch cost is shared by many layer-steps;
-one step per replay is reported as ``fuse_graph_1step``).  Reported beside
-it: eager timing, the same step with tables only as wide as the prompts,
-the split path (LIM -> scatter_copy -> SFA) eager and graph-replayed,
-per-kernel HIP-event times, the roofline of the index-key scan, the
-host-link rate of the miss copy, the CPU baseline on the same inputs, and
-rows for the other BASELINE configs and for the shapes of the reference's
-published tables (README_ops.md:281-324, Ascend 910C figures as context).
+is restored inside the timed region; the two queries are guarded against
+near-ties at every step's selection boundary, so the GPU's steps and the CPU
+chain's steps (``cpu_baseline.agreement``) must give the same miss counts,
+pool and HBM caches.  ``value`` is the median of three windows of K steps
+replayed from a captured HIP graph, one layer step per replay (the serving
+path replays graphs; one replay is exactly one step and the host submits
+nothing else).  Reported beside it: two steps per replay, eager steps (the
+reference's own perf method, ut_ops/test_fused_copy_sfa.py:720-734, here
+including the Python launch path's host time), the same step with tables
+only as wide as the prompts, the split path (LIM -> scatter_copy -> SFA)
+eager and graph-replayed, per-kernel HIP-event times, the roofline of the
+index-key scan, the host-link rate of the miss copy, the CPU baseline on the
+same inputs, and rows for the other BASELINE configs and for the shapes of
+the reference's published tables (README_ops.md:281-324, Ascend 910C figures
+as context).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 Prints one JSON line.
@@ -470,9 +474,10 @@ def main() -> int:
     B, N, C = 24, 32768, 2048
     tails = rng.integers(1, 128, size=B)
     t0 = time.time()
-    case = make_drift_case(B, N, C, tails, seed=args.seed, calib_device=dev)
-    log(f"bench: built cfg1 case in {time.time() - t0:.1f}s, target miss fractions "
-        f"{[round(x, 3) for x in case.meta['drift_miss_frac']]}")
+    verify_steps = args.cpu_steps + 1
+    case = make_drift_case(B, N, C, tails, seed=args.seed, calib_device=dev, guard=True, guard_steps=verify_steps)
+    log(f"bench: built cfg1 case in {time.time() - t0:.1f}s (guard halvings {case.meta['halvings']}), target miss "
+        f"fractions {[round(x, 3) for x in case.meta['drift_miss_frac']]}")
     cpu_case = case
     d = case.to_device(dev)
     scale = case.meta["scale"]
@@ -497,17 +502,41 @@ def main() -> int:
             f"last misses {int(t['miss_counts'].sum())}")
         return 0
 
+    # ---- the GPU's own steps from the initial state, for the comparison with
+    # the CPU chain's steps (cpu_baseline): miss counts per step, the pool and
+    # the HBM caches after the last step.  The inputs are guarded, so the two
+    # must agree exactly.
+    init = {k: t[k].clone() for k in ("cache_slots_pool", "hbm_kv_cache", "hbm_k_rope")}
+    verify_log = torch.zeros(verify_steps, B, dtype=torch.int32, device=dev)
+    head.run("fuse", verify_steps, miss_log=verify_log)
+    torch.cuda.synchronize()
+    gpu_verify = {"miss_counts": verify_log.cpu().numpy(),
+                  "pool": t["cache_slots_pool"].cpu().numpy(),
+                  "hbm_kv_cache": t["hbm_kv_cache"].cpu(), "hbm_k_rope": t["hbm_k_rope"].cpu(),
+                  "attention_out": t["attention_out"].float().cpu()}
+    for k, v in init.items():
+        t[k].copy_(v)
+    head.parity = 0
+    del init
+    torch.cuda.synchronize()
+
     miss_log = torch.zeros(args.steps, B, dtype=torch.int32, device=dev)
     head.run("fuse", max(args.warmup, 2))  # eager warmup
     torch.cuda.synchronize()
+
+    # ---- timed region: K graph-replayed layer steps, one step per replay
+    # (each replay is exactly one layer step; the host submits nothing else),
+    # three windows, the median.  Eager steps and two steps per replay are
+    # reported beside it.
     fuse_graphs = head.capture(torch, "fuse")
     head.replay_singles(fuse_graphs, args.warmup)
     torch.cuda.synchronize()
-
-    # ---- timed region: K graph-replayed layer steps (two per replay) --------
-    graph_ms, wall_ms = head.time_pairs(torch, fuse_graphs, args.steps)
-    graph1_ms = head.time_singles(torch, fuse_graphs, args.steps)
-    eager_ms = head.time_eager(torch, "fuse", args.steps)
+    windows = [head.time_singles(torch, fuse_graphs, args.steps) for _ in range(3)]
+    graph1_ms = float(np.median(windows))
+    pairs = [head.time_pairs(torch, fuse_graphs, args.steps) for _ in range(3)]
+    graph_ms = float(np.median([x[0] for x in pairs]))
+    wall_ms = float(np.median([x[1] for x in pairs]))
+    eager_ms = float(np.median([head.time_eager(torch, "fuse", args.steps) for _ in range(3)]))
 
     # ---- per-kernel HIP-event timing (eager, instrumented) ------------------
     with _lib.KernelTimer(capacity=16 * args.steps) as kt_fuse:
@@ -561,7 +590,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cpu_case, queries_cpu=[cpu_case["query_index_b"], cpu_case["query_index"]],
-                           steps=args.cpu_steps)
+                           steps=args.cpu_steps, gpu_verify=gpu_verify)
 
     rows = None
     if not args.no_rows:
@@ -579,7 +608,7 @@ def main() -> int:
         for name in ROW_NAMES:
             rows[name] = ROW_FUNCS[name](torch, np, dev, args.seed)
 
-    value_us = graph_ms * 1000.0
+    value_us = graph1_ms * 1000.0
     t_cap = 65536
     line = {
         "metric": METRIC,
@@ -588,7 +617,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(graph_ms, 4),
+        "ms_per_step": round(graph1_ms, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -598,7 +627,8 @@ def main() -> int:
             "workload": "BASELINE configs[1]: offload_fuse layer-step (fused_li_manage -> fused_copy_sfa), "
                         "bs=24, prompts 32768, C=2048, tails U[1,127], 32 index heads x 128, 64 attn heads "
                         "512+64, miss 5-15%/request, model-runner table layout (512-column block tables, "
-                        "65536-wide slot pool), HIP-graph replay",
+                        "65536-wide slot pool), HIP-graph replay of one layer step, median of 3 windows of K "
+                        "steps",
             "batch": B, "prompt_tokens": N, "cache_tokens": C, "index_heads": 32, "attn_heads": 64,
             "source_capacity": int(t_cap),
             "mean_tail": float(np.mean(tails)), "mean_miss_rows_per_step": round(miss_rows, 1),
@@ -616,8 +646,9 @@ def main() -> int:
             "scatter_copy_GBs": round(scatter_h2d, 2), "scatter_frac_of_measured": round(scatter_h2d / h2d_peak, 4),
         },
         "breakdown_us": {
-            "fuse_graph_step": round(value_us, 2), "fuse_graph_1step": round(graph1_ms * 1000, 2),
-            "fuse_eager_step": round(eager_ms * 1000, 2),
+            "fuse_graph_1step_replay": round(graph1_ms * 1000, 2),
+            "fuse_graph_1step_windows": [round(x * 1000, 2) for x in windows],
+            "fuse_graph_2step_replay": round(graph_ms * 1000, 2), "fuse_eager_step": round(eager_ms * 1000, 2),
             "fuse_graph_step_narrow_tables": round(narrow_ms * 1000, 2),
             "lim_manage_narrow_tables": round(sum(kt_narrow.mean_ms(n) for n in _ran(kt_narrow, MANAGE_KERNELS)) * 1000, 2),
             "split_graph_step": round(split_graph_ms * 1000, 2),
@@ -1114,7 +1145,7 @@ def measure_persist(torch, dev, seed: int, reps: int = 5):
             "frac_of_measured": round(rate / d2h, 3)}
 
 
-def cpu_baseline(case, queries_cpu, steps: int):
+def cpu_baseline(case, queries_cpu, steps: int, gpu_verify=None):
     """The layer-step on the host cores: oracle/torch_chain.py, the
     vectorised PyTorch-CPU chain (batched fp32 products for the scores and
     the attention, torch.topk, sorts and scatters for the slot bookkeeping,
@@ -1122,7 +1153,13 @@ def cpu_baseline(case, queries_cpu, steps: int):
     alternating queries as the GPU steps.  Median of ``steps`` layer-steps
     after one warmup, on min(16, os.cpu_count()) threads (the box's CPU
     share).  The numpy oracle (the tests' checker, per-request loops) is
-    timed for two steps beside it."""
+    timed for two steps beside it.
+
+    ``gpu_verify`` holds the GPU's own steps from the same initial state
+    (miss counts per step, then the pool, the HBM caches and the attention
+    output after the last step); the comparison with these CPU steps is
+    returned under ``agreement`` (the inputs are guarded at every step, so
+    the integers must agree exactly)."""
     import numpy as np
     import torch
 
@@ -1135,6 +1172,7 @@ def cpu_baseline(case, queries_cpu, steps: int):
     B = case.meta["batch"]
     scale = case.meta["scale"]
     times = []
+    cpu_misses = []
     for i in range(steps + 1):
         t0 = time.perf_counter()
         TC.fused_li_manage(queries_cpu[i % 2], t["index_weights"], t["index_key_cache"], t["index_block_table"],
@@ -1145,8 +1183,30 @@ def cpu_baseline(case, queries_cpu, steps: int):
                           t["dram_block_table"], t["hbm_k_rope"], t["hbm_kv_cache"], t["dram_k_rope"],
                           t["dram_kv_cache"], scale, t["attention_out"])
         times.append(time.perf_counter() - t0)
+        cpu_misses.append(t["miss_counts"].numpy().copy())
         log(f"bench: cpu torch chain step {i}: {times[-1] * 1e3:.1f} ms misses={int(t['miss_counts'].sum())}")
     med = float(np.median(times[1:]))
+    agreement = None
+    if gpu_verify is not None:
+        gm = gpu_verify["miss_counts"]
+        cm = np.stack(cpu_misses)
+        pool = t["cache_slots_pool"].numpy()
+        gpool = gpu_verify["pool"]
+        a = gpu_verify["attention_out"].double().numpy()
+        g = t["attention_out"].double().numpy()
+        agreement = {
+            "steps": int(cm.shape[0]),
+            "miss_counts_per_step_equal": bool(gm.shape == cm.shape and np.array_equal(gm, cm)),
+            "misses_per_step": [int(x) for x in cm.sum(axis=1)],
+            "pool_equal": bool(np.array_equal(gpool[:, :pool.shape[1]], pool)),
+            "hbm_caches_equal": bool(torch.equal(gpu_verify["hbm_kv_cache"].view(torch.int16),
+                                                 t["hbm_kv_cache"].view(torch.int16))
+                                     and torch.equal(gpu_verify["hbm_k_rope"].view(torch.int16),
+                                                     t["hbm_k_rope"].view(torch.int16))),
+            "attention_max_abs": float(np.abs(a - g).max()),
+            "attention_mean_rel": float(np.abs(a - g).mean() / max(np.abs(g).mean(), 1e-30)),
+        }
+        log(f"bench: cpu/gpu agreement {agreement}")
     # the numpy oracle, two steps on fresh state
     b16 = lambda x: x.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
     i32 = lambda x: x.numpy().copy()  # noqa: E731
@@ -1175,6 +1235,7 @@ def cpu_baseline(case, queries_cpu, steps: int):
                   f"of oracle/torch_chain.py (vectorised PyTorch-CPU, fp32) after 1 warmup, same inputs and "
                   f"alternating queries as the GPU steps; torch threads={threads}, os.cpu_count={os.cpu_count()}",
         "numpy_oracle_us": round(float(np.mean(otimes)) * 1e6, 1),
+        "agreement": agreement,
     }
 
 ROW_FUNCS = {

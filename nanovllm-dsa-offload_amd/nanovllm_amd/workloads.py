@@ -140,6 +140,8 @@ def make_chain_case(
     source_capacity: int | None = None,
     table_pad: int = -1,
     fast_fill: bool = False,
+    structured_orders=None,
+    miss_fracs=None,
 ) -> ChainCase:
     """One layer step.  ``source_lens`` / ``cache_tokens`` / ``tails`` are
     per-request lists (or scalars); source lengths are whole 128-token
@@ -154,7 +156,11 @@ def make_chain_case(
     :747-752; max_model_len = 65536 by default, nanovllm/config.py:68).
     ``table_pad`` fills the block-table columns past a request's blocks (the
     runner pads with 0).  ``fast_fill`` draws the large N(0,1) tensors with
-    :func:`randn_fill` (different values from the serial generator)."""
+    :func:`randn_fill` (different values from the serial generator).
+    ``structured_orders`` (with ``structured_scores``) gives each query row
+    its own weights for the key's base-64 digits (see
+    :func:`structured_query`), so that the rows select different sets.
+    ``miss_fracs`` (one per request) replaces the draw from ``miss_frac``."""
     B = int(batch)
     as_list = lambda v: [int(x) for x in (v if hasattr(v, "__len__") else [v] * B)]  # noqa: E731
     N = as_list(source_lens)
@@ -198,11 +204,8 @@ def make_chain_case(
             rows[:, 3] = (ids // 262144).float()
             keys[index_table[b, : nblk[b]].long()] = rows.view(nblk[b], BLOCK, 1, IDX)
         key_cache = keys.to(dtype)
-        q_index = torch.zeros(B * Q, index_heads, IDX)
-        q_index[:, 0, 0] = 1.0
-        q_index[:, 0, 1] = 64.0
-        q_index[:, 0, 2] = 4096.0
-        q_index[:, 0, 3] = 262144.0
+        orders = structured_orders if structured_orders is not None else [(1.0, 64.0, 4096.0, 262144.0)] * Q
+        q_index = torch.stack([structured_query(orders[r % len(orders)], index_heads) for r in range(B * Q)])
         q_index = q_index.to(dtype)
         weights = torch.zeros(B * Q, index_heads)
         weights[:, 0] = 1.0
@@ -286,6 +289,8 @@ def make_chain_case(
         else:
             union = sel_rows[0]
         frac = rng.uniform(*miss_frac)
+        if miss_fracs is not None:
+            frac = float(miss_fracs[b])
         m = int(round(frac * union.size))
         m = max(0, min(m, union.size, n - c))
         miss_target.append(m)
@@ -406,6 +411,49 @@ def make_chain_case(
     return ChainCase(tensors, meta)
 
 
+def structured_query(order, heads: int = 32) -> torch.Tensor:
+    """One index query row over the closed-form keys of
+    :func:`make_chain_case` (``structured_scores``: a token's key holds its
+    base-64 digits t % 64, (t >> 6) % 64, (t >> 12) % 64, t >> 18 in dims
+    0-3; ut_ops/test_fused_li_manage.py:146-173): head 0 weights the digits
+    by ``order``, every other head is zero.  With the weights (1, 0, ...)
+    the score is sum_i order[i] * digit_i, an integer below 2^24 whenever
+    the weights are distinct powers of 64: exact in fp32 under any
+    summation order, and distinct for distinct tokens."""
+    q = torch.zeros(heads, IDX)
+    q[0, :4] = torch.tensor([float(x) for x in order])
+    return q
+
+
+# Digit weights of the structured MTP3 drift queries: the six orders of the
+# three low digits (the fourth digit is 0 below 262144 tokens).
+STRUCTURED_ORDERS = {
+    "t": (1.0, 64.0, 4096.0, 0.0), "d0": (4096.0, 1.0, 64.0, 0.0), "d1": (1.0, 4096.0, 64.0, 0.0),
+    "d0d2": (64.0, 1.0, 4096.0, 0.0), "d1d0": (64.0, 4096.0, 1.0, 0.0), "d0d1": (4096.0, 64.0, 1.0, 0.0),
+}
+
+
+def make_structured_drift_case(batch: int, source_lens, cache_tokens, tails, orders_a, orders_b, *, mtp: bool = True,
+                               seed: int = 0, dtype: torch.dtype = torch.bfloat16, fast_fill: bool = False,
+                               source_capacity: int | None = None) -> ChainCase:
+    """Two alternating index queries over the closed-form index: query row
+    j of ``query_index`` weights the key digits by ``orders_a[j]``, of
+    ``query_index_b`` by ``orders_b[j]`` (:func:`structured_query`).  The
+    scores are exact integers, so every step's selection and victims are
+    the same under any fp32 summation order without a guard (victim-key ties
+    are exact too, and go to the lower slot by the canonical rule).  The pool
+    starts with ``query_index``'s union cached (plus the highest-scoring
+    other tokens up to C); the HBM cache matches it."""
+    case = make_chain_case(batch, source_lens, cache_tokens, tails, miss_frac=(0.0, 0.0), seed=seed, dtype=dtype,
+                           guard=False, mtp=mtp, structured_scores=True, structured_orders=list(orders_a),
+                           fast_fill=fast_fill, source_capacity=source_capacity)
+    Q = case.meta["queries"]
+    B = case.meta["batch"]
+    case.tensors["query_index_b"] = torch.stack(
+        [structured_query(orders_b[r % Q], case.tensors["query_index"].shape[1]) for r in range(B * Q)]).to(dtype)
+    return case
+
+
 RUNNER_CAPACITY = 65536  # default max_model_len (nanovllm/config.py:68), in tokens
 
 
@@ -483,21 +531,37 @@ def make_drift_case(
     index_heads: int = 32,
     attn_heads: int = 64,
     calib_device=None,
+    mtp: bool = False,
+    guard: bool = False,
+    guard_steps: int = 8,
+    guard_first: str = "query_index_b",
+    fast_fill: bool = False,
+    source_capacity: int | None = None,
 ) -> ChainCase:
-    """Steady-state decode workload for benchmarking.
+    """Steady-state decode workload: two index queries that alternate.
 
-    Adds a second index query ``query_index_b`` per request, a perturbation
-    of ``query_index`` calibrated (bisection on the perturbation size) so
-    that its top-2048 set differs from the first query's by the request's
-    target miss fraction drawn from ``miss_frac``.  The pool starts with the
-    first query's top-C cached; alternating the two queries step after step
-    then makes every step miss ~that fraction, with the HBM cache kept
-    consistent by the copies themselves -- no state restore between steps.
+    Adds a second index query ``query_index_b`` per request (MTP3: per query
+    row, one perturbation size shared by a request's four rows), a
+    perturbation of ``query_index`` calibrated (bisection on the
+    perturbation size) so that its top-2048 set (MTP3: the union of the four
+    rows' sets) differs from the first query's by the request's target miss
+    fraction drawn from ``miss_frac``.  The pool starts with the first
+    query's top-C cached; alternating the two queries step after step then
+    makes every step miss ~that fraction, with the HBM cache kept consistent
+    by the copies themselves -- no state restore between steps.
+
+    ``guard=True`` makes every step of ``guard_steps`` alternating steps
+    (``guard_first`` first, starting from the initial pool) well defined
+    under any fp32 summation order: see :func:`guard_alternating_steps`
+    (for MTP3 cases, whose eight rows make its halvings cascade, see
+    :func:`make_structured_drift_case`).
     """
     case = make_chain_case(batch, source_lens, cache_tokens, tails, miss_frac=(0.0, 0.0), seed=seed, dtype=dtype,
-                           guard=False, index_heads=index_heads, attn_heads=attn_heads)
+                           guard=False, index_heads=index_heads, attn_heads=attn_heads, mtp=mtp,
+                           fast_fill=fast_fill, source_capacity=source_capacity)
     t = case.tensors
     B = case.meta["batch"]
+    Q = MTP_Q if mtp else 1
     rng = np.random.default_rng(seed + 7)
     g = torch.Generator().manual_seed(seed + 7)
     dev = torch.device(calib_device) if calib_device is not None else torch.device("cpu")
@@ -507,34 +571,200 @@ def make_drift_case(
     table = t["index_block_table"].to(dev)
     qb = torch.empty_like(t["query_index"])
     achieved = []
+
+    def selected(keys, qrows, wrows, n):
+        mask = torch.zeros(n, dtype=torch.bool, device=dev)
+        for j in range(Q):
+            mask[torch.topk(_torch_scores(keys, qrows[j], wrows[j]), TOPK).indices] = True
+        return mask
+
     for b in range(B):
         n = case.meta["source_lens"][b]
+        rows = slice(b * Q, b * Q + Q)
         if n <= TOPK or case.meta["cache_tokens"][b] < TOPK:
-            qb[b] = t["query_index"][b]
+            qb[rows] = t["query_index"][rows]
             achieved.append(0.0)
             continue
         tok = torch.arange(n, device=dev)
         keys = kc[table[b, tok // BLOCK].long() * BLOCK + tok % BLOCK]
-        top_a = torch.topk(_torch_scores(keys, qa[b], w[b]), TOPK).indices
-        in_a = torch.zeros(n, dtype=torch.bool, device=dev)
-        in_a[top_a] = True
-        eps = torch.randn(qa[b].shape, generator=g).to(dev)
+        in_a = selected(keys, qa[rows], w[rows], n)
+        eps = torch.randn(qa[rows].shape, generator=g).to(dev)
         target = rng.uniform(*miss_frac)
         lo, hi = 0.0, 2.0
-        best = (1.0, qa[b].to(dtype), 0.0)
+        best = (1.0, qa[rows].to(dtype), 0.0)
         for _ in range(14):
             mid = 0.5 * (lo + hi)
-            cand = (qa[b] + mid * eps).to(dtype)
-            top_b = torch.topk(_torch_scores(keys, cand.float(), w[b]), TOPK).indices
-            frac = float((~in_a[top_b]).sum()) / TOPK
+            cand = (qa[rows] + mid * eps).to(dtype)
+            in_b = selected(keys, cand.float(), w[rows], n)
+            frac = float((in_b & ~in_a).sum()) / float(in_b.sum())
             if abs(frac - target) < abs(best[0] - target):
                 best = (frac, cand, mid)
             if frac < target:
                 lo = mid
             else:
                 hi = mid
-        qb[b] = best[1].cpu()
+        qb[rows] = best[1].cpu()
         achieved.append(best[0])
     t["query_index_b"] = qb
     case.meta["drift_miss_frac"] = achieved
+    case.meta["guard_steps"] = 0
+    if guard:
+        names = ("query_index_b", "query_index")
+        if guard_first not in names:
+            raise ValueError(f"guard_first must be one of {names}")
+        names = names if guard_first == names[0] else names[::-1]
+        case.meta["halvings"] += guard_alternating_steps(case, names, guard_steps)
+        case.meta["guard_steps"] = guard_steps
+        case.meta["guard_first"] = guard_first
     return case
+
+
+class _RowWindow:
+    """The ``TOPK + window`` highest-scoring tokens of one query row in
+    descending order (ties to the lower token), kept up to date while tokens
+    are halved: a halved token leaves the window and re-enters at its new
+    place only if it still ranks inside it.  The order of the other tokens
+    does not change, so no re-sort is needed."""
+
+    def __init__(self, scores: np.ndarray, window: int = 1024) -> None:
+        self.s = scores
+        self.window = window
+        self.refresh()
+
+    def refresh(self) -> None:
+        self.top = [int(x) for x in _topk_order(self.s, TOPK + self.window)]
+        self.member = set(self.top)
+
+    def halved(self, tok: int) -> None:
+        if tok not in self.member:
+            return
+        self.top.remove(tok)
+        self.member.discard(tok)
+        last = self.top[-1]
+        v = self.s[tok]
+        if v > self.s[last] or (v == self.s[last] and tok < last):
+            lo, hi = 0, len(self.top)
+            while lo < hi:  # first position whose token ranks below tok
+                mid = (lo + hi) // 2
+                u = self.top[mid]
+                if self.s[u] > v or (self.s[u] == v and u < tok):
+                    lo = mid + 1
+                else:
+                    hi = mid
+            self.top.insert(lo, tok)
+            self.member.add(tok)
+        if len(self.top) < TOPK + 2:
+            self.refresh()
+
+
+def guard_alternating_steps(case: ChainCase, query_names, steps: int, max_halvings: int | None = None) -> int:
+    """Make ``steps`` consecutive LIM steps well defined under any fp32
+    summation order, step i using ``query_names[i % len(query_names)]``,
+    the slot pool carried from step to step (no restore), starting from the
+    case's pool.
+
+    With float64 scores and a per-token bound on the fp32 reduction error
+    (the bound of :func:`make_chain_case`), it requires:
+
+    * for every query row of every query tensor, a gap larger than the two
+      tokens' bounds between the 2048th and 2049th largest scores (these do
+      not depend on the carried state);
+    * at every step where the victims are not forced (more cached tokens
+      outside the selection than misses), a gap larger than the bounds
+      between the last victim and the first kept token by the victim key
+      (MTP3: the largest of the step's four row scores), the cached set
+      followed through the steps.
+
+    Where a gap is too small it halves the index key of the token just
+    outside the selection (or the last victim), which scales that token's
+    scores by exactly 1/2 for every query, and checks again.  The slots need
+    no guard: pairing victims with misses is an integer rule.
+
+    The error bound spans about ten score spacings at a 32K-token boundary,
+    so a boundary is cleared by halving the ~10 tokens below it.  With one
+    row per query tensor (MTP0) the two tensors' boundaries sit among the
+    same tokens and that is all.  With eight rows (MTP3) a halved token is
+    often inside another row's selection, whose boundary then moves by one
+    and needs its own ~10 halvings: the halvings cascade through the whole
+    prompt, and the limit (2n halvings per request) raises an error.
+    Returns the number of halvings."""
+    t = case.tensors
+    B = case.meta["batch"]
+    Q = case.meta["queries"]
+    mtp = case.meta["mtp"]
+    dtype = t["index_key_cache"].dtype
+    kc = t["index_key_cache"].view(-1, IDX)
+    table = t["index_block_table"]
+    pool = t["cache_slots_pool"]
+    halvings = 0
+    for b in range(B):
+        n, c = case.meta["source_lens"][b], case.meta["cache_tokens"][b]
+        active = (n > TOPK and c >= TOPK and c <= n) if not mtp else (n > TOPK and c >= min(n, 8192) and c <= n)
+        if not active:
+            continue
+        limit = max_halvings if max_halvings is not None else 2 * n
+        tok = torch.arange(n)
+        phys = table[b, tok // BLOCK].long() * BLOCK + tok % BLOCK
+        k = _f64(kc[phys])
+        ka = np.abs(k)
+        s, e, win = {}, {}, []
+        for name in query_names:
+            qq = _f64(t[name][b * Q:(b + 1) * Q])      # [Q, H, 128]
+            ww = _f64(t["index_weights"][b * Q:(b + 1) * Q])
+            s[name] = np.stack([np.maximum(k @ qq[j].T, 0.0) @ ww[j] for j in range(Q)])
+            e[name] = np.stack([_ERR_UNIT * (ka @ np.abs(qq[j]).T) @ np.abs(ww[j]) for j in range(Q)])
+            win += [(name, j, _RowWindow(s[name][j])) for j in range(Q)]
+        row = pool[t["req_pool_entries"][b]].numpy()[:n]
+        cached0 = (row >= 0) & (row < c)
+        count = [0]
+
+        def halve(z: int) -> None:
+            if count[0] >= limit:
+                raise RuntimeError(f"request {b}: no well-defined step sequence after {limit} halvings")
+            kc[phys[z]] = (kc[phys[z]].float() * 0.5).to(dtype)
+            for name in query_names:
+                s[name][:, z] *= 0.5
+                e[name][:, z] *= 0.5
+            for _, _, w in win:
+                w.halved(z)
+            count[0] += 1
+
+        while True:
+            changed = True
+            while changed:
+                changed = False
+                for name, j, w in win:
+                    while True:
+                        a, z = w.top[TOPK - 1], w.top[TOPK]
+                        if s[name][j, a] - s[name][j, z] >= e[name][j, a] + e[name][j, z] + 1e-12:
+                            break
+                        halve(z)
+                        changed = True
+            union = {name: np.zeros(n, bool) for name in query_names}
+            for name, _, w in win:
+                union[name][np.asarray(w.top[:TOPK])] = True
+            bad = None
+            cached = cached0.copy()
+            for step in range(steps):
+                name = query_names[step % len(query_names)]
+                sel = union[name]
+                misses = np.nonzero(sel & ~cached)[0]
+                cand = np.nonzero(cached & ~sel)[0]
+                m = misses.size
+                if 0 < m < cand.size:
+                    smax, emax = s[name].max(axis=0), e[name].max(axis=0)
+                    order = cand[np.lexsort((cand, smax[cand]))]
+                    lo, hi = order[m - 1], order[m]
+                    if smax[hi] - smax[lo] < emax[lo] + emax[hi] + 1e-12:
+                        bad = int(lo)
+                        break
+                    victims = order[:m]
+                else:
+                    victims = cand[:m]
+                cached[victims] = False
+                cached[misses] = True
+            if bad is None:
+                break
+            halve(bad)
+        halvings += count[0]
+    return halvings

@@ -88,6 +88,45 @@ def oracle_chain(case, lim, mtp: bool):
     return gold, hkpe, hckv
 
 
+def oracle_steps(case, query_names, mtp: bool):
+    """The oracle through consecutive LIM -> copy -> attention steps with
+    the pool and the HBM caches carried from step to step (no restore);
+    step i uses the index query tensor ``query_names[i]``.  Returns one
+    dict per step: the LIM outputs (``check_lim`` keys) and the pool after
+    the step, the HBM cache bits after the copy, and the float64 golden."""
+    t = case.tensors
+    dt = dname(t["query_index"].dtype)
+    B = t["num_candidate_tokens"].shape[0]
+    R = t["topk_src_ids"].shape[0]
+    pool = ints(t["cache_slots_pool"])
+    hkpe, hckv = bits(t["hbm_k_rope"]), bits(t["hbm_kv_cache"])
+    fixed = (bits(t["index_weights"]), bits(t["index_key_cache"]), ints(t["index_block_table"]),
+             ints(t["num_candidate_tokens"]), ints(t["num_cache_tokens"]), ints(t["req_pool_entries"]))
+    attn = (bits(t["query_rope"]), bits(t["query"]), ints(t["actual_seq_lengths_kv"]), ints(t["num_cache_tokens"]))
+    tables = (ints(t["hbm_block_table"]), ints(t["dram_block_table"]))
+    dram = (bits(t["dram_k_rope"]), bits(t["dram_kv_cache"]))
+    out = []
+    for name in query_names:
+        src = np.full((R, 1, TOPK), -1, np.int32)
+        dst = np.full((R, 1, TOPK), -1, np.int32)
+        mc = np.zeros(B, np.int32)
+        if mtp:
+            ms = np.full((B, 8192), -1, np.int32)
+            md = np.full((B, 8192), -1, np.int32)
+            O.fused_li_manage_mtp(bits(t[name]), *fixed, pool, src, dst, ms, md, mc, dtype=dt)
+            lim = dict(src=src, dst=dst, miss_src=ms, miss_dst=md, miss_counts=mc)
+            gold = O.fused_copy_sfa_mtp(*attn, dst, ms, md, mc, *tables, hkpe, hckv, *dram, case.meta["scale"],
+                                        dtype=dt)
+        else:
+            O.fused_li_manage(bits(t[name]), *fixed, pool, src, dst, mc, dtype=dt)
+            lim = dict(src=src, dst=dst, miss_counts=mc)
+            gold = O.fused_copy_sfa(*attn, dst, src.reshape(B, TOPK), mc, *tables, hkpe, hckv, *dram,
+                                    case.meta["scale"], dtype=dt)
+        lim["pool"] = pool.copy()
+        out.append(dict(lim=lim, hkpe=hkpe.copy(), hckv=hckv.copy(), gold=gold, query=name))
+    return out
+
+
 def widen_layout(t: dict, capacity: int, pad: int = 0) -> dict:
     """The model runner's table layout (nanovllm_amd.workloads.caller_layout)."""
     from nanovllm_amd.workloads import caller_layout

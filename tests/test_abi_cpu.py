@@ -243,11 +243,36 @@ def test_persist_validation():
 
 
 def test_torch_library_schemas_match_reference():
+    """Every schema torch registered for nanovllm_dsa hashes to the digest of
+    the reference's own string (tests/golden/reference_schemas.json, written
+    by tests/golden/make_schema_digests.py from bindings/nanovllm_ops.cpp:645-714),
+    and, where the reference checkout is present, equals that string."""
+    import hashlib
+    import json
+    from pathlib import Path
+
     from nanovllm_amd import ops
 
-    for name, schema in ops.SCHEMAS.items():
+    golden = json.loads((Path(__file__).parent / "golden" / "reference_schemas.json").read_text())["sha256"]
+    assert set(golden) == set(ops.SCHEMAS)
+    registered = {}
+    for name in ops.SCHEMAS:
         op = getattr(torch.ops.nanovllm_dsa, name).default
-        assert str(op._schema) == "nanovllm_dsa::" + schema
+        text = str(op._schema)
+        assert text.startswith("nanovllm_dsa::")
+        registered[name] = text[len("nanovllm_dsa::"):]
+        assert hashlib.sha256(registered[name].encode()).hexdigest() == golden[name], name
+    ref = Path("/root/reference")
+    if ref.exists():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("make_schema_digests",
+                                                      Path(__file__).parent / "golden" / "make_schema_digests.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        theirs = mod.reference_schemas(ref)
+        for name, text in registered.items():
+            assert theirs[name] == text, name
 
 
 def test_meta_dispatch_returns_none():

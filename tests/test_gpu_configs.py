@@ -88,7 +88,7 @@ def test_cfg1_bs24_32k():
 
 
 def test_cfg2_bs64_mixed_20k_64k():
-    _run_config(2, (None,), ("fused", "split"))
+    _run_config(2, (None, CALLER_CAPACITY), ("fused", "split"))
 
 
 def test_cfg3_mtp3_bs16x4_48k():
