@@ -61,7 +61,7 @@ PCIE_PEAK_GBS = 64.0           # PCIe Gen5 x16 per direction (published)
 ROW_BYTES = (512 + 64) * 2     # one latent KV row (CKV + KPE)
 KEY_ROW_BYTES = 128 * 2        # one index-key row
 ROW_NAMES = ("cfg0_bs1", "cfg3_mtp3", "cfg2_bs64_mixed", "cfg4_indexshare", "ref_lim_bs24_64k",
-             "ref_copysfa_bs24_4heads", "lidu_init", "indexer_project", "prefill_persist")
+             "ref_copysfa_bs24_4heads", "lidu_init", "indexer_project", "prefill_persist", "miss_copy_dma")
 
 
 def log(msg: str) -> None:
@@ -400,6 +400,94 @@ def measure_ref_copysfa(torch, np, dev, seed: int, steps: int = 20):
     out["fused_h2d_GBs"] = round(copy_bytes / (out["kernels_us"]["sfa_split_kernel_fused"] * 1e-6) / 1e9, 2)
     out["ascend_910c_context_ms"] = {k: v for k, v in REF_910C.items() if k.endswith("_ms")}
     del ch, d, case
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_copy_dma(torch, np, dev, seed: int, reps: int = 3):
+    """The miss copy of one cfg1 step by the DMA engines instead of the GPU's
+    loads: one hipMemcpyAsync per miss row and part (the 1024-byte CKV and
+    the 128-byte KPE rows are scattered, so no larger copy exists), on one
+    side stream and spread over four, against the same rows gathered by
+    scatter_copy and one contiguous hipMemcpyAsync of the same bytes.  The
+    DMA path needs the miss list on the host, a device-to-host copy and a
+    synchronisation that the chain does not have (and that graph capture
+    excludes); that part is left out of these figures.  The process's HIP
+    runtime (torch's) exports no batched copy (hipMemcpyBatchAsync)."""
+    import ctypes
+
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import caller_layout, make_drift_case
+
+    rng = np.random.default_rng(1001)
+    B = 24
+    case = make_drift_case(B, 32768, 2048, rng.integers(1, 128, size=B), seed=seed, calib_device=dev)
+    d = case.to_device(dev)
+    ch = Chain(caller_layout(d.tensors), case.meta["scale"])
+    ch.run("lim", 1)  # the first step's query: real misses
+    torch.cuda.synchronize()
+    t = ch.t
+    mc = t["miss_counts"].cpu().numpy()
+    src, dst = ch.src2d.cpu().numpy(), ch.dst2d.cpu().numpy()
+    dtab, htab = t["dram_block_table"].cpu().numpy(), t["hbm_block_table"].cpu().numpy()
+    drow = np.concatenate([dtab[b, src[b, :mc[b]] >> 7] * 128 + (src[b, :mc[b]] & 127) for b in range(B)])
+    hrow = np.concatenate([htab[b, dst[b, :mc[b]] >> 7] * 128 + (dst[b, :mc[b]] & 127) for b in range(B)])
+    n = int(drow.size)
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime already loaded in this process
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    hip.hipMemcpyAsync.restype = ctypes.c_int
+    h2d = 1  # hipMemcpyHostToDevice
+    ckv_h, kpe_h = t["dram_kv_cache_host"].data_ptr(), t["dram_k_rope_host"].data_ptr()
+    ckv_d, kpe_d = t["hbm_kv_cache"].data_ptr(), t["hbm_k_rope"].data_ptr()
+    pairs = [(ckv_d + int(h) * 1024, ckv_h + int(s) * 1024, 1024) for s, h in zip(drow, hrow)] + \
+            [(kpe_d + int(h) * 128, kpe_h + int(s) * 128, 128) for s, h in zip(drow, hrow)]
+    out = {"workload": f"the {n} miss rows of one cfg1 step (bs=24, 32768, C=2048), {n * ROW_BYTES} bytes",
+           "miss_rows": n}
+    for nstreams in (1, 4):
+        streams = [torch.cuda.Stream() for _ in range(nstreams)]
+        gpu_ms, host_ms = [], []
+        for _ in range(reps):
+            t["hbm_kv_cache"].view(-1, 512)[torch.from_numpy(hrow).to(dev)] = 0
+            torch.cuda.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in streams]
+            for st, (e0, _) in zip(streams, ev):
+                e0.record(st)
+            w0 = time.perf_counter()
+            for i, (dp, sp, nb) in enumerate(pairs):
+                rc = hip.hipMemcpyAsync(dp, sp, nb, h2d, streams[i % nstreams].cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"hipMemcpyAsync failed: {rc}")
+            host_ms.append((time.perf_counter() - w0) * 1e3)
+            for st, (_, e1) in zip(streams, ev):
+                e1.record(st)
+            torch.cuda.synchronize()
+            gpu_ms.append(max(e0.elapsed_time(e1) for e0, e1 in ev))
+        got = t["hbm_kv_cache"].view(-1, 512)[torch.from_numpy(hrow).to(dev)].cpu()
+        want = t["dram_kv_cache_host"].view(-1, 512)[torch.from_numpy(drow)]
+        us = float(np.median(gpu_ms)) * 1000
+        out[f"dma_{nstreams}_streams"] = {"gpu_us": round(us, 1), "GBs": round(n * ROW_BYTES / (us * 1e-6) / 1e9, 2),
+                                          "host_submit_us": round(float(np.median(host_ms)) * 1000, 1),
+                                          "copies": len(pairs), "bytes_equal": bool(torch.equal(got, want))}
+    with _lib.KernelTimer(capacity=4 * reps) as kt:
+        for _ in range(reps):
+            ch.scatter()
+        torch.cuda.synchronize()
+    us = kt.mean_ms("scatter_copy_kernel") * 1000
+    out["scatter_copy_kernel"] = {"gpu_us": round(us, 1), "GBs": round(n * ROW_BYTES / (us * 1e-6) / 1e9, 2)}
+    nb = n * ROW_BYTES
+    hbuf = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+    dbuf = torch.empty(nb, dtype=torch.uint8, device=dev)
+    dbuf.copy_(hbuf, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dbuf.copy_(hbuf, non_blocking=True)
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1000 / reps
+    out["one_contiguous_memcpy"] = {"gpu_us": round(us, 1), "GBs": round(nb / (us * 1e-6) / 1e9, 2)}
+    del ch, d, case, hbuf, dbuf
     torch.cuda.empty_cache()
     return out
 
@@ -1248,6 +1336,7 @@ ROW_FUNCS = {
     "lidu_init": measure_lidu_init,
     "indexer_project": lambda torch, np, dev, seed: measure_indexer(torch, dev, seed),
     "prefill_persist": lambda torch, np, dev, seed: measure_persist(torch, dev, seed),
+    "miss_copy_dma": measure_copy_dma,
 }
 
 
