@@ -794,7 +794,10 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
         t["cache_slots_pool"].copy_(pool0)
         if i == 1:
             _lib.xcd_roles(reset=True)
-        step()
+            with _lib.record_xcd_roles():
+                step()
+        else:
+            step()
     # the XCDs the overlap kernel's copy and attention workgroups ran on in the second warm-up step
     # (one launch: the dispatcher's starting XCD may differ between launches)
     copy_xcds, attn_xcds = _lib.xcd_roles(reset=True)

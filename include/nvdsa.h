@@ -403,6 +403,9 @@ const char* nvdsa_kernel_name(int32_t kernel_id);
  * the speed depends on it.  With reset != 0 the record is cleared after the
  * read.  Synchronises the device; not for use under graph capture. */
 int nvdsa_xcd_roles(uint32_t* masks, int32_t reset);
+/* Turns that record on (on != 0) or off for the launches made from then on
+ * (a captured graph keeps the setting of its capture). */
+void nvdsa_xcd_roles_record(int32_t on);
 
 #ifdef __cplusplus
 }

@@ -53,6 +53,7 @@ constexpr int kHistBins = 1 << kHistBits;
 constexpr int kGatherPart = 128;                  // MTP0: in-bin tokens a chunk can hand over
 constexpr int kRankDirect = 512;                  // MTP0: in-bin tokens ranked pairwise by the last chunk
 constexpr int kMissPart = 256;                    // MTP0: definite misses a chunk can hand over
+constexpr int kInBinScan = 64;                    // MTP0 last chunk: longer in-bin miss lists are sorted
 constexpr int kSpecChunks = 16;                   // MTP0 last chunk: requests of up to this many chunks ...
 constexpr int kSpecEntries = 64;                  // ... read this many definite misses per chunk up front
 constexpr int kSpecGather = 16;                   // ... and this many in-bin tokens
@@ -1468,16 +1469,52 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       pool[t] = d;
     }
   };
-  for (int f = tid; f < nd; f += kManageThreads) {
-    const int p = chunk_of(L.doff, active, f);
-    if (L.cdm[p] > kMissPart) continue;  // placed by the ordered pass below
-    const int t = L.dmiss[f];
+  // In-bin misses of chunk p below token t.  A short list is scanned; a long
+  // one (a cold pool row with many ties at the threshold: up to 2048 entries,
+  // every miss scanning them would serialise on this workgroup) is sorted once
+  // and searched.
+  const bool ib_sorted = nib > kInBinScan;
+  if (ib_sorted) {
+    int np2 = kInBinScan;
+    while (np2 < nib) np2 <<= 1;  // <= kTopK: at most k in-bin tokens are selected
+    for (int i = nib + tid; i < np2; i += kManageThreads) L.ibm[i] = INT_MAX;
+    lds_barrier();
+    for (int size = 2; size <= np2; size <<= 1)  // bitonic sort, ascending
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < np2 / 2; i += kManageThreads) {
+          const int pos = 2 * i - (i & (stride - 1));
+          const int x = L.ibm[pos], y = L.ibm[pos + stride];
+          if ((x > y) == ((pos & size) == 0)) {
+            L.ibm[pos] = y;
+            L.ibm[pos + stride] = x;
+          }
+        }
+        lds_barrier();
+      }
+  }
+  auto lower = [&](int t) {  // sorted in-bin misses below t
+    int lo_i = 0, hi_i = nib;
+    while (lo_i < hi_i) {
+      const int mid = (lo_i + hi_i) >> 1;
+      if (L.ibm[mid] < t) lo_i = mid + 1;
+      else hi_i = mid;
+    }
+    return lo_i;
+  };
+  auto ib_before = [&](int t, int p) {
+    if (ib_sorted) return lower(t) - lower(p * kChunk);
     int before_ib = 0;
     for (int j = 0; j < nib; ++j) {
       const int x = L.ibm[j];
       before_ib += (x < t && x >= p * kChunk) ? 1 : 0;
     }
-    emit(L.goff[p] + (f - L.doff[p]) + before_ib, t);
+    return before_ib;
+  };
+  for (int f = tid; f < nd; f += kManageThreads) {
+    const int p = chunk_of(L.doff, active, f);
+    if (L.cdm[p] > kMissPart) continue;  // placed by the ordered pass below
+    const int t = L.dmiss[f];
+    emit(L.goff[p] + (f - L.doff[p]) + ib_before(t, p), t);
   }
   for (int j = tid; j < nib; j += kManageThreads) {
     const int t = L.ibm[j];
@@ -1490,12 +1527,7 @@ __device__ __forceinline__ void mtp0_resolve(const LimArgs& a, const LimWs& w, i
       if (L.dmiss[mid] < t) lo_i = mid + 1;
       else hi_i = mid;
     }
-    int before_ib = 0;
-    for (int j2 = 0; j2 < nib; ++j2) {
-      const int x = L.ibm[j2];
-      before_ib += (x < t && x >= p * kChunk) ? 1 : 0;
-    }
-    emit(L.goff[p] + (lo_i - L.doff[p]) + before_ib, t);
+    emit(L.goff[p] + (lo_i - L.doff[p]) + ib_before(t, p), t);
   }
   if (miss_over) {
     // Chunks with more definite misses than their slice: one ordered pass

@@ -190,6 +190,8 @@ const char* nvdsa_kernel_name(int32_t kernel_id) {
   return names[kernel_id];
 }
 
+void nvdsa_xcd_roles_record(int32_t on) { nvdsa::sfa_xcd_roles_record(on != 0); }
+
 int nvdsa_xcd_roles(uint32_t* masks, int32_t reset) {
   if (masks == nullptr) return fail(NVDSA_ERR_ARG, "xcd_roles: masks must not be null");
   const hipError_t err = nvdsa::sfa_xcd_roles(masks, reset != 0);
@@ -242,8 +244,14 @@ void* noalloc_scratch(int device, const char* op) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[device] == nullptr) {
+    // A first call made while the caller captures a graph: the lookup enqueues
+    // nothing, but the runtime may load the code object; this thread's capture
+    // mode is relaxed for the lookup so that the capture stays valid.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool exchanged = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (exchanged) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || ptr == nullptr) {
       fail(NVDSA_ERR_RUNTIME,
            (std::string(op) + ": hipGetSymbolAddress(scratch) failed: " + hipGetErrorString(e)).c_str());

@@ -182,6 +182,8 @@ hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream);
 // copy ([0]) and attention ([1]) workgroups ran on; clears it after the read
 // when `reset`.  Synchronises the device.
 hipError_t sfa_xcd_roles(uint32_t masks[2], bool reset);
+// Whether launches made from now on write that record (off by default).
+void sfa_xcd_roles_record(bool on);
 
 // ---- indexer projection (decode query rows and head weights) -------------
 struct IndexerArgs {

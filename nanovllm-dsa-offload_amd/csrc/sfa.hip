@@ -40,6 +40,7 @@
 //   others attend the keys already in HBM, and a second launch attends the
 //   copied keys.
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 
 #include "nvdsa_common.h"
@@ -136,8 +137,11 @@ constexpr int kCopyWgs = kCopyXcds * 32;
 // (bit x of [0]: a copy workgroup ran on XCD x; of [1]: an attention
 // workgroup), one copy per device, read by sfa_xcd_roles.  The roles are
 // given by linear workgroup id on the assumption that the dispatcher deals
-// workgroups to the XCDs round-robin; the masks show whether it did.
+// workgroups to the XCDs round-robin; the masks show whether it did.  Only
+// launches made while recording is on (sfa_xcd_roles_record, a diagnostic)
+// write them: the serving path does no diagnostic writes.
 __device__ unsigned int g_xcd_roles[2];
+std::atomic<int> g_record_xcd_roles{0};
 
 // Id of the XCD the calling wave runs on (hardware register XCC_ID, bits 3:0).
 __device__ inline unsigned int hw_xcd_id() {
@@ -602,11 +606,12 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 template <typename T>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void sfa_mtp_overlap_kernel(SfaArgs a, Partials part, int splits,
                                                                        int splits_total, ScatterArgs sc,
-                                                                       int attn_blocks, int hgroups, int copy_wgs) {
+                                                                       int attn_blocks, int hgroups, int copy_wgs,
+                                                                       int record_roles) {
   const int p = blockIdx.x;
   const int xcd = p & 7;
   const int slot = p >> 3;
-  if (threadIdx.x == 0) atomicOr(&g_xcd_roles[xcd < kCopyXcds ? 0 : 1], 1u << hw_xcd_id());
+  if (record_roles != 0 && threadIdx.x == 0) atomicOr(&g_xcd_roles[xcd < kCopyXcds ? 0 : 1], 1u << hw_xcd_id());
   if (xcd < kCopyXcds) {
     // The copy moves 16-pair chunks with 4 waves (scatter_copy_wg); the
     // workgroup's other waves have nothing to copy.
@@ -772,7 +777,8 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
   const int attn_blocks = static_cast<int>(rows * s1);
   const int64_t slots = std::max(ceil_div(kCopyWgs, kCopyXcds), ceil_div(attn_blocks * hgroups, 8 - kCopyXcds));
   launch_kernel(kKernSfaMtpOverlap, sfa_mtp_overlap_kernel<T>, dim3(static_cast<uint32_t>(8 * slots)),
-                dim3(kAttnThreads), stream, a, p, s1, total, sc, attn_blocks, static_cast<int>(hgroups), kCopyWgs);
+                dim3(kAttnThreads), stream, a, p, s1, total, sc, attn_blocks, static_cast<int>(hgroups), kCopyWgs,
+                g_record_xcd_roles.load(std::memory_order_relaxed));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_kernel(kKernSfaSplitCopied, sfa_split_kernel<T, false, kKeysCopied>,
@@ -804,6 +810,8 @@ hipError_t launch_fused_copy_sfa(const SfaArgs& a, hipStream_t stream) {
     return a.elem == Elem::kBf16 ? launch_fused_mtp<Bf16>(a, stream) : launch_fused_mtp<F16>(a, stream);
   return a.elem == Elem::kBf16 ? launch_sfa<Bf16, true>(a, stream) : launch_sfa<F16, true>(a, stream);
 }
+
+void sfa_xcd_roles_record(bool on) { g_record_xcd_roles.store(on ? 1 : 0, std::memory_order_relaxed); }
 
 hipError_t sfa_xcd_roles(uint32_t masks[2], bool reset) {
   hipError_t err = hipDeviceSynchronize();

@@ -80,6 +80,7 @@ SIGNATURES = {
                            ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
     "nvdsa_kernel_name": ([ctypes.c_int32], ctypes.c_char_p),
     "nvdsa_xcd_roles": ([ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32], ctypes.c_int),
+    "nvdsa_xcd_roles_record": ([ctypes.c_int32], None),
 }
 
 
@@ -170,6 +171,19 @@ class KernelTimer:
     def mean_ms(self, name: str) -> float:
         vals = [ms for k, ms in self.records if k == name]
         return sum(vals) / len(vals) if vals else float("nan")
+
+
+class record_xcd_roles:
+    """Context manager: the MTP3 overlap kernels launched inside the block
+    record the XCDs their workgroup roles ran on (nvdsa_xcd_roles_record);
+    recording is off again afterwards.  Read the record with xcd_roles."""
+
+    def __enter__(self):
+        lib.nvdsa_xcd_roles_record(1)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        lib.nvdsa_xcd_roles_record(0)
 
 
 def xcd_roles(reset: bool = False) -> tuple[int, int]:

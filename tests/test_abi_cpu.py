@@ -20,7 +20,7 @@ def test_library_exports_every_header_symbol():
     from nanovllm_amd import _lib
 
     declared = _lib.exported_symbols_from_header(HEADER)
-    assert len(declared) == 25, declared
+    assert len(declared) == 26, declared
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}

@@ -244,7 +244,10 @@ def test_fused_copy_sfa_mtp_roles_on_separate_xcds():
     case = _chain_after_lim(make_chain_case(2, [4096, 6144], [2048, 2048], [4, 33], seed=3, mtp=True), mtp=True)
     d = case.to_device("cuda")
     _lib.xcd_roles(reset=True)
-    _run_fused(d, case.meta["scale"], mtp=True)
+    _run_fused(d, case.meta["scale"], mtp=True)  # recording off: no record
+    assert _lib.xcd_roles(reset=True) == (0, 0)
+    with _lib.record_xcd_roles():
+        _run_fused(d, case.meta["scale"], mtp=True)
     copy_xcds, attn_xcds = _lib.xcd_roles(reset=True)
     print(f"copy XCDs {copy_xcds:#04x}, attention XCDs {attn_xcds:#04x}", flush=True)
     assert copy_xcds & attn_xcds == 0, (hex(copy_xcds), hex(attn_xcds))

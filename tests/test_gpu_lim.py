@@ -292,6 +292,25 @@ def _assert_matches(d, expect, mtp):
     assert np.array_equal(ints(d["cache_slots_pool"]), expect["pool"])
 
 
+@pytest.mark.parametrize("n_tokens", [4096, 12288, 40960])
+def test_lim_ties_on_cold_rows_bit_exact(n_tokens):
+    """Cold pool rows (nothing cached) with a 2048th score shared by
+    thousands of tokens: every selected tied token is an in-bin miss (1348
+    per row here), so the last chunk orders a long in-bin miss list (sorted,
+    then searched) against the definite misses."""
+    case = _tie_case(False, [700], n_tokens=n_tokens)
+    t = case.tensors
+    for row in ints(t["req_pool_entries"]):
+        t["cache_slots_pool"][int(row)].fill_(-1)
+    print(f"LIM ties on cold rows N={n_tokens}", flush=True)
+    expect = oracle_lim(case)
+    valid = np.asarray(case.meta["cache_tokens"]) <= n_tokens  # (C > N disables a row: miss_counts 0)
+    assert (expect["miss_counts"][valid] == TOPK).all() and (expect["miss_counts"][~valid] == 0).all()
+    d = case.to_device("cuda", host_mapped=False)
+    _run_lim(d)
+    _assert_matches(d, expect, False)
+
+
 @pytest.mark.parametrize("mtp,positives,n_tokens", TIE_CASES)
 def test_lim_unmapped_index_blocks_score_lowest(mtp, positives, n_tokens):
     """Index block-table entries that name no key block (-1, or at or past

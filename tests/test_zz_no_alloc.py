@@ -9,6 +9,12 @@ registers, longer ones streamed) and cache budgets whose slot tables live in
 the scratch memory; the second reuses the scratch memory the first left
 behind.  A batch whose scratch would exceed the static size is rejected
 before anything is launched.
+
+Under HIP-graph capture: the call captured, then replayed on two different
+inputs written into the captured tensors, each replay bit-exact with the
+workspace entry point on the same inputs; and, in a fresh process, the same
+with the first call of that process (the one that looks the scratch address
+up) made while capturing.
 """
 
 from __future__ import annotations
@@ -80,6 +86,71 @@ def test_noalloc_matches_workspace_entry_point_twice():
     small = make_chain_case(2, [8192, 4096], [2048, 2048], [3, 9], seed=72)
     _compare(big, "call 1 (6 requests, S_cap 65536)")
     _compare(small, "call 2 (2 requests, S_cap 8192)", with_oracle=True)
+
+
+INPUTS = ("query_index", "index_weights", "index_key_cache", "index_block_table", "num_candidate_tokens",
+          "num_cache_tokens", "req_pool_entries", "cache_slots_pool")
+
+
+def _poison(t) -> None:
+    for k in ("topk_src_ids", "topk_dst_slots", "miss_counts"):
+        t[k].fill_(-5)
+
+
+def capture_check(label: str) -> None:
+    """Capture nvdsa_fused_li_manage_noalloc in a graph, replay it on two
+    inputs and compare each replay with the workspace entry point."""
+    from nanovllm_amd import _lib
+    from nanovllm_amd.workloads import make_chain_case
+
+    lens, caches, tails = [8192, 20480, 4096], [2048, 4096, 2048], [3, 9, 1]
+    cases = [make_chain_case(3, lens, caches, tails, seed=s) for s in (73, 74)]
+    g = cases[0].to_device("cuda").tensors
+    _poison(g)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print(f"NOALLOC {label}: capture", flush=True)
+    with torch.cuda.graph(graph):
+        assert _call(g, True) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert (ints(g["miss_counts"]) == -5).all(), "capture ran the call"
+    for i, case in enumerate(cases):
+        ref = case.to_device("cuda").tensors
+        assert _call(ref, False) == 0, _lib.last_error()
+        for k in INPUTS:
+            g[k].copy_(case.tensors[k].to("cuda"))
+        _poison(g)
+        torch.cuda.synchronize()
+        print(f"NOALLOC {label}: replay {i}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        for k in OUTS:
+            assert np.array_equal(ints(g[k]), ints(ref[k])), (label, i, k)
+        assert int(ints(g["miss_counts"]).sum()) > 0, (label, i)
+    del graph
+
+
+def test_noalloc_captured_in_a_graph():
+    capture_check("graph")
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process():
+    """The scratch address is looked up on a device's first call; here that
+    call is made while capturing (a fresh process: no earlier call)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    here = Path(__file__).resolve().parent
+    code = (f"import sys; sys.path[:0] = [{str(here)!r}, {str(here.parent / 'nanovllm-dsa-offload_amd')!r}, "
+            f"{str(here.parent)!r}]\n"
+            "import test_zz_no_alloc as T\n"
+            "T.capture_check('first call under capture')\n"
+            "print('FIRST CALL UNDER CAPTURE OK', flush=True)\n")
+    print("NOALLOC fresh process: start", flush=True)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
+    print(out.stdout[-2000:], out.stderr[-2000:], flush=True)
+    assert out.returncode == 0 and "FIRST CALL UNDER CAPTURE OK" in out.stdout
 
 
 def test_noalloc_rejects_scratch_beyond_its_size():
