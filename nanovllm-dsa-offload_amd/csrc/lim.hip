@@ -141,6 +141,33 @@ __device__ inline bool lim_mtp_row_valid(int n, int c, int r, int64_t cap, int64
 // Order-preserving 32-bit key of a score (one zero: -0 and +0 rank equal).
 __device__ inline uint32_t score_key(float s) { return float_key(s == 0.f ? 0.f : s); }
 
+// Smallest and largest of lo / hi over the wave's 64 lanes, left in lane 63:
+// butterflies within each row of 16 lanes, then the row broadcasts (DPP
+// moves: VALU only, no LDS-routed shuffles).
+template <int CTRL, int ROW_MASK>
+__device__ inline void minmax_dpp_step(uint32_t& lo, uint32_t& hi) {
+  lo = min(lo, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(lo), static_cast<int>(lo), CTRL,
+                                                                 ROW_MASK, 0xf, false)));
+  hi = max(hi, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(hi), static_cast<int>(hi), CTRL,
+                                                                 ROW_MASK, 0xf, false)));
+}
+__device__ inline void wave_minmax_to_lane63(uint32_t& lo, uint32_t& hi) {
+  minmax_dpp_step<0xb1, 0xf>(lo, hi);   // quad_perm [1,0,3,2]
+  minmax_dpp_step<0x4e, 0xf>(lo, hi);   // quad_perm [2,3,0,1]
+  minmax_dpp_step<0x141, 0xf>(lo, hi);  // row_half_mirror
+  minmax_dpp_step<0x140, 0xf>(lo, hi);  // row_mirror: every lane holds its row's result
+  minmax_dpp_step<0x142, 0xa>(lo, hi);  // row_bcast:15 (rows 1 and 3 take rows 0 and 2)
+  minmax_dpp_step<0x143, 0xc>(lo, hi);  // row_bcast:31 (rows 2 and 3 take rows 0-1)
+}
+
+// Sum of x and the value of lane i ^ 32 (v_permlane32_swap: a VALU exchange
+// of the wave's halves instead of an LDS-routed shuffle).  Both lanes of a
+// pair get the same sum.
+__device__ inline float add_lane_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---------------------------------------------------------------------------
 // 1. Scores.
 // RELU = false is the first-decode initialisation score (no ReLU,
@@ -289,7 +316,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
     uint32_t klo = 0xffffffffu, khi = 0u;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      float s = part[tt] + __shfl_xor(part[tt], 32, 64);
+      float s = add_lane_xor32(part[tt]);
       if (s == 0.f) s = 0.f;  // one zero: -0 and +0 rank equal
       const int64_t t = t0 + tt * 32 + col_lane;
       if (grp == 0 && t < n) {
@@ -302,12 +329,8 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
     }
     if constexpr (kRanges) {
       if (brange != nullptr) {
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-          klo = min(klo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(klo), d, 64)));
-          khi = max(khi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(khi), d, 64)));
-        }
-        if (lane == 0) *brange = make_uint2(klo, khi);
+        wave_minmax_to_lane63(klo, khi);
+        if (lane == kWave - 1) *brange = make_uint2(klo, khi);
       }
     }
   }

@@ -265,8 +265,13 @@ def _tie_case(mtp: bool, positives, seed=11, n_tokens=12288):
 
 # MTP0: at 4096 tokens the 3396 tied zeros fit the threshold bin's gather
 # list; at 12288 and 40960 they overflow it and the last chunk streams the row.
+# MTP3: with fewer than 2048 positive tokens per query row the threshold is
+# the 0 shared by thousands of tokens; with more, it falls among the 128
+# distinct positive values, each held by ~16-70 tokens, so a few of the ties
+# at the threshold are selected and the cutoff falls inside a run of them.
 TIE_CASES = [(False, [700], 4096), (False, [700], 12288), (False, [700], 40960),
-             (True, [500, 900, 1300, 1900], 12288)]
+             (True, [500, 900, 1300, 1900], 12288), (True, [2100, 2600, 3000, 4000], 12288),
+             (True, [2100, 3000, 5000, 9000], 40960)]
 
 
 @pytest.mark.parametrize("mtp,positives,n_tokens", TIE_CASES)
