@@ -69,7 +69,8 @@ constexpr int kMissSplits = 2;  // fused: least splits of a row that take its ho
 constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgroups per launch
 constexpr int kFusedMaxSplits = 16;  // fused: most splits per row from kFusedCapRows rows on
 constexpr int kFusedCapRows = 8;
-constexpr int kFusedTargetWgs = 128;  // fused: workgroups per launch from kFusedCapRows rows on
+constexpr int kFusedTargetWgs = 128;  // fused: workgroups per launch above kFusedCapRows rows
+constexpr int kFusedTargetWgsSmall = 96;  // fused: workgroups per launch at kFusedCapRows rows
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -725,17 +726,21 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
   // From kFusedCapRows rows on, the fused kernel lasts as long as its
   // host-link-bound miss splits, so its HBM splits can take more tiles each:
-  // about 128 workgroups in all, 4 to kFusedMaxSplits splits per row, keep
-  // the partials (128 KB per split and row at 64 heads) and their merge
-  // small while the HBM-only splits still end before the copies (8 rows: 16
-  // splits, combine 6.9 -> 4.2 us; 24 rows: 6 splits, combine 7.0 -> 5.7 us
-  // and the step 3 us shorter; the fused kernel no slower in either).  With
-  // fewer rows the HBM tiles are the longer path and keep every split
-  // (1 row: 64).
+  // about 128 workgroups in all (96 at kFusedCapRows rows), 4 to
+  // kFusedMaxSplits splits per row, keep the partials (128 KB per split and
+  // row at 64 heads) and their merge small while the HBM-only splits still
+  // end before the copies.  Measured: 24 rows, 6 splits (10 before): combine
+  // 7.0 -> 5.7 us and the step 3 us shorter (4 splits: the fused kernel 4 us
+  // longer); 8 rows, 12 splits (32, then 16 before): the fused kernel 53.5
+  // -> 51.9 us, combine 4.9 -> 4.6 us, the 78-layer step 5.60 -> 5.48 ms
+  // (9 splits: 5.55 ms).  With fewer rows the HBM tiles are the longer path
+  // and keep every split (1 row: 64).
   int splits = choose_splits(rows, hgroups);
-  if (FUSED && rows >= kFusedCapRows)
+  if (FUSED && rows >= kFusedCapRows) {
+    const int target = rows * hgroups <= kFusedCapRows ? kFusedTargetWgsSmall : kFusedTargetWgs;
     splits = std::min<int>(splits, std::max<int>(4, std::min<int>(kFusedMaxSplits, static_cast<int>(ceil_div(
-                                                                  kFusedTargetWgs, rows * hgroups)))));
+                                                                  target, rows * hgroups)))));
+  }
   SfaArgs args = a;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
   launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED, kKeysAll>,
