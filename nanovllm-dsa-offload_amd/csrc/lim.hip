@@ -356,14 +356,10 @@ struct SelectOut {
 // only.
 template <bool LDS_ONLY = false>
 __device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, uint32_t* red) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    lo = min(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), d, 64)));
-    hi = max(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), d, 64)));
-  }
+  wave_minmax_to_lane63(lo, hi);
   const int wid = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
+  if ((threadIdx.x & 63) == kWave - 1) {
     red[2 * wid] = lo;
     red[2 * wid + 1] = hi;
   }
@@ -497,9 +493,14 @@ __device__ SelectOut radix_select(int ngroups, int k, uint32_t kmin, uint32_t km
 // Bitwise OR of one word per thread over the workgroup, with barriers that
 // order LDS only.  `scratch` must hold blockDim/64 ints.
 __device__ inline unsigned block_or_lds(unsigned v, int* scratch) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v |= static_cast<unsigned>(__shfl_xor(static_cast<int>(v), d, 64));
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = static_cast<int>(v);
+  // The wave's OR in lane 63: the DPP steps of wave_minmax_to_lane63.
+  v |= dpp_u32<0xb1, 0xf, 0xf, false>(v);
+  v |= dpp_u32<0x4e, 0xf, 0xf, false>(v);
+  v |= dpp_u32<0x141, 0xf, 0xf, false>(v);
+  v |= dpp_u32<0x140, 0xf, 0xf, false>(v);
+  v |= dpp_u32<0x142, 0xa, 0xf, false>(v);
+  v |= dpp_u32<0x143, 0xc, 0xf, false>(v);
+  if ((threadIdx.x & 63) == kWave - 1) scratch[threadIdx.x >> 6] = static_cast<int>(v);
   lds_barrier();
   unsigned r = 0u;
   for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) r |= static_cast<unsigned>(scratch[w]);
@@ -523,13 +524,7 @@ __device__ inline uint64_t block_exclusive_scan4(uint64_t v, uint64_t* scratch, 
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  uint64_t x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t lo = __shfl_up(static_cast<uint32_t>(x), d, 64);
-    const uint32_t hi = __shfl_up(static_cast<uint32_t>(x >> 32), d, 64);
-    if (lane >= d) x += (static_cast<uint64_t>(hi) << 32) | lo;
-  }
+  const uint64_t x = wave_inclusive_scan(v);
   if (lane == 63) scratch[wid] = x;
   scan_barrier<LDS_ONLY>();
   uint64_t before = 0, tot = 0;
@@ -551,22 +546,13 @@ __device__ inline int lane16(uint64_t v, int q) { return static_cast<int>((v >> 
 
 // Exclusive block scan of eight packed 16-bit counters (two 64-bit words;
 // every counter's block total must stay below 65536).  One pass for all
-// eight: the wave scans shuffle 32-bit halves, the 8 wave totals go through
+// eight: DPP wave scans of the 64-bit words, the 8 wave totals go through
 // LDS.  Totals are wave-uniform.
 __device__ inline void block_exclusive_scan8(uint64_t (&v)[2], uint64_t* scratch, uint64_t (&total)[2]) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  uint64_t x[2] = {v[0], v[1]};
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t lo = __shfl_up(static_cast<uint32_t>(x[h]), d, 64);
-      const uint32_t hi = __shfl_up(static_cast<uint32_t>(x[h] >> 32), d, 64);
-      if (lane >= d) x[h] += (static_cast<uint64_t>(hi) << 32) | lo;
-    }
-  }
+  const uint64_t x[2] = {wave_inclusive_scan(v[0]), wave_inclusive_scan(v[1])};
   if (lane == 63) {
     scratch[2 * wid] = x[0];
     scratch[2 * wid + 1] = x[1];

@@ -111,6 +111,41 @@ __device__ inline void scan_barrier() {
     __syncthreads();
 }
 
+// Inclusive prefix sums over the wave's 64 lanes on the VALU: DPP row shifts
+// build each 16-lane row's prefix (shifts 1, 2, 3, then 4 into banks 1-3 and 8
+// into banks 2-3), and the row broadcasts add the rows before (lane 15 into
+// rows 1 and 3, lane 31 into rows 2 and 3).  Lanes a step leaves out add 0.
+// (The LDS-routed shuffles they replace wait one LDS round trip per step.)
+template <int CTRL, int ROW_MASK, int BANK_MASK, bool BOUND_ZERO>
+__device__ inline uint32_t dpp_u32(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO));
+}
+template <int CTRL, int ROW_MASK, int BANK_MASK, bool BOUND_ZERO>
+__device__ inline uint64_t dpp_u64(uint64_t x) {
+  const uint32_t lo = dpp_u32<CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO>(static_cast<uint32_t>(x));
+  const uint32_t hi = dpp_u32<CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO>(static_cast<uint32_t>(x >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+template <typename U, int CTRL, int ROW_MASK, int BANK_MASK, bool BOUND_ZERO>
+__device__ inline U dpp_any(U x) {
+  if constexpr (sizeof(U) == 8)
+    return dpp_u64<CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO>(x);
+  else
+    return dpp_u32<CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO>(x);
+}
+template <typename U>
+__device__ inline U wave_inclusive_scan(U x) {
+  U s = x + dpp_any<U, 0x111, 0xf, 0xf, true>(x);  // row_shr:1
+  s += dpp_any<U, 0x112, 0xf, 0xf, true>(x);       // row_shr:2
+  s += dpp_any<U, 0x113, 0xf, 0xf, true>(x);       // row_shr:3
+  s += dpp_any<U, 0x114, 0xf, 0xe, true>(s);       // row_shr:4, lanes 4-15 of each row
+  s += dpp_any<U, 0x118, 0xf, 0xc, true>(s);       // row_shr:8, lanes 8-15
+  s += dpp_any<U, 0x142, 0xa, 0xf, false>(s);      // row_bcast:15 into rows 1 and 3
+  s += dpp_any<U, 0x143, 0xc, 0xf, false>(s);      // row_bcast:31 into rows 2 and 3
+  return s;
+}
+
 // Block-wide exclusive prefix sum of one int per thread (blockDim <= 1024,
 // multiple of 64).  `scratch` must hold blockDim/64 + 1 ints.  Returns the
 // exclusive prefix; *total receives the block sum.  Every thread reads the
@@ -122,13 +157,7 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int* total) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  // inclusive wave scan via shuffles
-  int x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
+  const int x = static_cast<int>(wave_inclusive_scan(static_cast<uint32_t>(v)));
   if (lane == 63) scratch[wid] = x;
   scan_barrier<LDS_ONLY>();
   int before = 0, tot = 0;
