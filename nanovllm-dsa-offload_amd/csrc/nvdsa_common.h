@@ -1,6 +1,8 @@
 // Shared constants and device helpers of the gfx950 DSA offload kernels.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -145,6 +147,42 @@ __device__ inline U wave_inclusive_scan(U x) {
   s += dpp_any<U, 0x143, 0xc, 0xf, false>(s);      // row_bcast:31 into rows 2 and 3
   return s;
 }
+
+// Cross-lane combines on the VALU.  v_permlane16_swap / v_permlane32_swap
+// with the value in both operands leave the values of lanes i and i ^ 16
+// (i ^ 32) in the two results, in the same order for both lanes of a pair,
+// so a commutative op gives both lanes the same result.
+template <typename Op>
+__device__ inline float xor16_op(float x, Op op) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <typename Op>
+__device__ inline float xor32_op(float x, Op op) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// op over all 64 lanes, in every lane: butterflies within each row of 16
+// lanes (DPP quad permutes and mirrors), then across rows.
+template <typename Op>
+__device__ inline float wave_all_op(float x, Op op) {
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), decltype(ctrl)::value, 0xf,
+                                                      0xf, false));
+  };
+  x = op(x, dpp(x, std::integral_constant<int, 0xb1>{}));   // quad_perm [1,0,3,2]
+  x = op(x, dpp(x, std::integral_constant<int, 0x4e>{}));   // quad_perm [2,3,0,1]
+  x = op(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  x = op(x, dpp(x, std::integral_constant<int, 0x140>{}));  // row_mirror
+  x = xor16_op(x, op);
+  return xor32_op(x, op);
+}
+struct MaxOp {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct AddOp {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
 
 // Block-wide exclusive prefix sum of one int per thread (blockDim <= 1024,
 // multiple of 64).  `scratch` must hold blockDim/64 + 1 ints.  Returns the

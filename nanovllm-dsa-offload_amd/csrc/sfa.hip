@@ -513,8 +513,7 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
             sv[kt * 4 + i] = x;
             mx = fmaxf(mx, x);
           }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = xor32_op(xor16_op(mx, MaxOp{}), MaxOp{});
         // The reference max only moves when the tile max exceeds it by more
         // than kMaxSlack (base-2 units), so P stays below 2^kMaxSlack and the
         // numerator is rescaled on few tiles (softmax does not depend on the
@@ -572,8 +571,7 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   // wave its 256 latent dims; the pair's (max, sum) are equal, half 0
   // writes them).
   if (!wave_active || head >= a.heads) return;
-  float lsum = l_run + __shfl_xor(l_run, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  const float lsum = xor32_op(xor16_op(l_run, AddOp{}), AddOp{});
   if (g == 0 && half == 0) {
     part.ml[pidx * 2 + 0] = m_run;
     part.ml[pidx * 2 + 1] = lsum;
@@ -664,16 +662,14 @@ __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(Sf
   if (lane + kWave < splits) v1 = mlp[base + (lane + kWave) * H];
   const bool live0 = v0.y > 0.f, live1 = v1.y > 0.f;
   float m = fmaxf(live0 ? v0.x : -INFINITY, live1 ? v1.x : -INFINITY);
-#pragma unroll
-  for (int off = kWave / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  m = wave_all_op(m, MaxOp{});
   float w0 = 0.f, w1 = 0.f;
   if (m != -INFINITY) {
     w0 = live0 ? exp2f(v0.x - m) : 0.f;
     w1 = live1 ? exp2f(v1.x - m) : 0.f;
   }
   float total = (live0 ? v0.y * w0 : 0.f) + (live1 ? v1.y * w1 : 0.f);
-#pragma unroll
-  for (int off = kWave / 2; off >= 1; off >>= 1) total += __shfl_xor(total, off, kWave);
+  total = wave_all_op(total, AddOp{});
   // Consumed here, unconditionally: otherwise the compiler sinks each
   // split's load into its conditional use below, one wait each.
 #pragma unroll
