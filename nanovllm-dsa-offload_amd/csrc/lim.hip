@@ -141,31 +141,10 @@ __device__ inline bool lim_mtp_row_valid(int n, int c, int r, int64_t cap, int64
 // Order-preserving 32-bit key of a score (one zero: -0 and +0 rank equal).
 __device__ inline uint32_t score_key(float s) { return float_key(s == 0.f ? 0.f : s); }
 
-// Smallest and largest of lo / hi over the wave's 64 lanes, left in lane 63:
-// butterflies within each row of 16 lanes, then the row broadcasts (DPP
-// moves: VALU only, no LDS-routed shuffles).
-template <int CTRL, int ROW_MASK>
-__device__ inline void minmax_dpp_step(uint32_t& lo, uint32_t& hi) {
-  lo = min(lo, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(lo), static_cast<int>(lo), CTRL,
-                                                                 ROW_MASK, 0xf, false)));
-  hi = max(hi, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(hi), static_cast<int>(hi), CTRL,
-                                                                 ROW_MASK, 0xf, false)));
-}
+// Smallest and largest of lo / hi over the wave's 64 lanes, left in lane 63.
 __device__ inline void wave_minmax_to_lane63(uint32_t& lo, uint32_t& hi) {
-  minmax_dpp_step<0xb1, 0xf>(lo, hi);   // quad_perm [1,0,3,2]
-  minmax_dpp_step<0x4e, 0xf>(lo, hi);   // quad_perm [2,3,0,1]
-  minmax_dpp_step<0x141, 0xf>(lo, hi);  // row_half_mirror
-  minmax_dpp_step<0x140, 0xf>(lo, hi);  // row_mirror: every lane holds its row's result
-  minmax_dpp_step<0x142, 0xa>(lo, hi);  // row_bcast:15 (rows 1 and 3 take rows 0 and 2)
-  minmax_dpp_step<0x143, 0xc>(lo, hi);  // row_bcast:31 (rows 2 and 3 take rows 0-1)
-}
-
-// Sum of x and the value of lane i ^ 32 (v_permlane32_swap: a VALU exchange
-// of the wave's halves instead of an LDS-routed shuffle).  Both lanes of a
-// pair get the same sum.
-__device__ inline float add_lane_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  lo = wave_reduce_to_lane63(lo, MinU32Op{});
+  hi = wave_reduce_to_lane63(hi, MaxU32Op{});
 }
 
 // ---------------------------------------------------------------------------
@@ -316,7 +295,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
     uint32_t klo = 0xffffffffu, khi = 0u;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      float s = add_lane_xor32(part[tt]);
+      float s = xor32_op(part[tt], AddOp{});  // both halves of the head reduction
       if (s == 0.f) s = 0.f;  // one zero: -0 and +0 rank equal
       const int64_t t = t0 + tt * 32 + col_lane;
       if (grp == 0 && t < n) {
@@ -493,13 +472,7 @@ __device__ SelectOut radix_select(int ngroups, int k, uint32_t kmin, uint32_t km
 // Bitwise OR of one word per thread over the workgroup, with barriers that
 // order LDS only.  `scratch` must hold blockDim/64 ints.
 __device__ inline unsigned block_or_lds(unsigned v, int* scratch) {
-  // The wave's OR in lane 63: the DPP steps of wave_minmax_to_lane63.
-  v |= dpp_u32<0xb1, 0xf, 0xf, false>(v);
-  v |= dpp_u32<0x4e, 0xf, 0xf, false>(v);
-  v |= dpp_u32<0x141, 0xf, 0xf, false>(v);
-  v |= dpp_u32<0x140, 0xf, 0xf, false>(v);
-  v |= dpp_u32<0x142, 0xa, 0xf, false>(v);
-  v |= dpp_u32<0x143, 0xc, 0xf, false>(v);
+  v = wave_reduce_to_lane63(v, OrU32Op{});
   if ((threadIdx.x & 63) == kWave - 1) scratch[threadIdx.x >> 6] = static_cast<int>(v);
   lds_barrier();
   unsigned r = 0u;

@@ -177,6 +177,34 @@ __device__ inline float wave_all_op(float x, Op op) {
   x = xor16_op(x, op);
   return xor32_op(x, op);
 }
+// An idempotent op (min, max, or) over the wave's 64 lanes, left in lane 63:
+// butterflies within each row of 16 lanes (DPP quad permutes and mirrors),
+// then the row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2
+// and 3).  Lanes a broadcast leaves out combine with their own value.
+template <typename Op>
+__device__ inline uint32_t wave_reduce_to_lane63(uint32_t x, Op op) {
+  auto dpp = [](uint32_t v, auto ctrl, auto row_mask) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v),
+                                                             decltype(ctrl)::value, decltype(row_mask)::value, 0xf,
+                                                             false));
+  };
+  using std::integral_constant;
+  x = op(x, dpp(x, integral_constant<int, 0xb1>{}, integral_constant<int, 0xf>{}));   // quad_perm [1,0,3,2]
+  x = op(x, dpp(x, integral_constant<int, 0x4e>{}, integral_constant<int, 0xf>{}));   // quad_perm [2,3,0,1]
+  x = op(x, dpp(x, integral_constant<int, 0x141>{}, integral_constant<int, 0xf>{}));  // row_half_mirror
+  x = op(x, dpp(x, integral_constant<int, 0x140>{}, integral_constant<int, 0xf>{}));  // row_mirror
+  x = op(x, dpp(x, integral_constant<int, 0x142>{}, integral_constant<int, 0xa>{}));  // row_bcast:15
+  return op(x, dpp(x, integral_constant<int, 0x143>{}, integral_constant<int, 0xc>{}));  // row_bcast:31
+}
+struct MinU32Op {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; }
+};
+struct MaxU32Op {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
+struct OrU32Op {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a | b; }
+};
 struct MaxOp {
   __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
 };
