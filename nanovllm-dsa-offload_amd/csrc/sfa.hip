@@ -12,10 +12,11 @@
 //
 // Kernel design (split-KV flash decode):
 //   grid = rows x splits x ceil(heads/64); a 512-thread workgroup owns one
-//   row, one split of its key list and 64 heads.  Its 8 wavefronts are 4
-//   pairs, one pair per 16 heads; the two waves of a pair (two per SIMD,
-//   so one hides the other's LDS and MFMA latency) split the work by
-//   dimension: wave half d takes S's dims [288d, 288d + 288) and the
+//   row, one split of its key list and 64 heads (small non-fused launches:
+//   256-thread workgroups of 32 heads, two per CU, see AttnShape).  Its 8
+//   wavefronts are 4 pairs, one pair per 16 heads; the two waves of a pair
+//   (two per SIMD, so one hides the other's LDS and MFMA latency) split the
+//   work by dimension: wave half d takes S's dims [288d, 288d + 288) and the
 //   output's latent dims [256d, 256d + 256).  Keys are processed in tiles
 //   of 32.  Each lane keeps its query operand (one head, 9 x 16 bytes of
 //   its 288 dims) in registers for the whole split; each tile is gathered
@@ -51,18 +52,42 @@ namespace nvdsa {
 namespace {
 
 constexpr int kTileKeys = 32;
-constexpr int kAttnThreads = 512;
-constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr int kAttnThreads = 512;  // the fused and overlap kernels (AttnShape<8>)
 constexpr int kHeadsPerBlock = 64;
 constexpr int kKStride = kQkDim + 16;      // LDS row of the key tile (elements; 1184 B, fewest bank conflicts)
 constexpr int kChunksPerKey = kQkDim * 2 / 16;  // 72 x 16 bytes
-// Tile loads per thread: 2304 16-byte chunks over 512 threads (4.5 each).
-constexpr int kChunksPerThread = 5;
 constexpr int kSChunks = kQkDim / 32 / 2;  // 9 MFMA k-steps of 32 dims: one wave's half of S
 constexpr int kVDims = kCkvDim / 2;        // 256 latent dims of the output per wave
 constexpr int kMaxSplits = 64;
-constexpr int kWindowTiles = kAttnThreads / kTileKeys;  // tiles resolved per window (one key per thread)
-constexpr int kWindowKeys = kWindowTiles * kTileKeys;
+
+// Workgroup shapes of the split attention.  W waves form W/2 pairs, one pair
+// per 16 heads (the two waves of a pair split S and the output by dims).
+// * W = 8: 64 heads, one workgroup per CU, two tile buffers (the next tile
+//   is stored during the current one's PV).  The fused kernel (each host
+//   tile is read once, so all of a row's heads share it) and the MTP3
+//   overlap launch.
+// * W = 4: 32 heads, two workgroups per CU, one tile buffer (a third barrier
+//   per tile before the next tile is stored).  Small sparse_tail_attention
+//   and MTP3 copied-key launches (plan_split): twice the workgroups of the
+//   8-wave grid, and the two workgroups of a CU are not tied by one barrier.
+//   A row's two head halves read the same key tiles; they are launched on
+//   one XCD so the second read hits its L2.
+template <int W>
+struct AttnShape {
+  static_assert(W == 4 || W == 8, "split attention: 4 or 8 waves");
+  static constexpr int kThreads = 64 * W;
+  static constexpr int kPairs = W / 2;
+  static constexpr int kHeads = 16 * kPairs;
+  static constexpr int kBuffers = W == 8 ? 2 : 1;
+  static constexpr int kWindowTiles = kThreads / kTileKeys;  // tiles resolved per window (one key per thread)
+  static constexpr int kWindowKeys = kThreads;
+  // HBM tiles: 8 threads per key; a thread loads kCkvChunks 16-byte chunks of
+  // the latent row (W = 8: the waves of dim half d take chunks 4d..4d+3 of
+  // each 8; W = 4: all 8) and, in dim half 0, one of the rope part.
+  static constexpr int kCkvChunks = W == 8 ? 4 : 8;
+  // Host tiles (fused, W = 8 only): 2304 16-byte chunks over 512 threads.
+  static constexpr int kPf = W == 8 ? 5 : kCkvChunks + 1;  // tile chunks held per thread
+};
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxSlack = 8.f;  // base-2 headroom of the running max (P < 256)
 constexpr int kMissSplits = 2;  // fused: least splits of a row that take its host-sourced tiles
@@ -150,6 +175,14 @@ __device__ inline unsigned int hw_xcd_id() {
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
   return v;
 }
+// x extent of a split-attention grid of n (row, split) workgroups: 4-wave
+// launches round it up to a multiple of 8, so the head halves of a row's
+// split (x, 0) and (x, 1) are dealt to the same XCD.
+template <int W>
+int64_t split_grid_x(int64_t n) {
+  return W == 8 ? n : (n + 7) / 8 * 8;
+}
+
 int overlap_splits(int64_t rows, int64_t head_groups) {
   // About two workgroups per attention CU: the rows' tiles spread evenly.
   int64_t s = ceil_div(2 * (8 - kCopyXcds) * 32, rows * head_groups);
@@ -158,15 +191,38 @@ int overlap_splits(int64_t rows, int64_t head_groups) {
   return static_cast<int>(s);
 }
 
+// Splits per row for a launch of W-wave workgroups (head_groups of
+// AttnShape<W>::kHeads heads): the resident workgroups of the 256 CUs (one
+// per CU at W = 8, two at W = 4, as the register footprint allows) in a
+// single round.
+template <int W>
 int choose_splits(int64_t rows, int64_t head_groups) {
   if (rows <= 0 || head_groups <= 0) return 1;
-  // One resident workgroup per CU (the register footprint allows one): fill
-  // the 256 CUs in a single round.
-  const int64_t target = 256;
+  const int64_t target = W == 8 ? 256 : 512;
   int64_t s = target / (rows * head_groups);
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
   return static_cast<int>(s);
+}
+
+// Shape of a sparse_tail_attention or MTP3 copied-key launch.  4-wave
+// workgroups where the 8-wave grid leaves most CUs idle (at most two
+// (row, 64-head group) pairs: 64 splits each, up to 128 workgroups on 256
+// CUs), 8-wave ones otherwise.  Kernel times at 64 heads, 8 -> 4 waves:
+// 1 row 13.2 -> 10.5 us, 2 rows 15.3 -> 13.9, 3 rows 17.9 -> 17.5, 24 rows
+// 27.3 -> 29.8.
+struct SplitPlan {
+  int waves;
+  int splits;
+  int64_t hgroups;
+};
+SplitPlan plan_split(int64_t rows, int64_t heads) {
+  if (rows * ceil_div(heads, kHeadsPerBlock) <= 2) {
+    const int64_t hg = ceil_div(heads, AttnShape<4>::kHeads);
+    return {4, choose_splits<4>(rows, hg), hg};
+  }
+  const int64_t hg = ceil_div(heads, AttnShape<8>::kHeads);
+  return {8, choose_splits<8>(rows, hg), hg};
 }
 
 // Key selection of a split-attention launch over a row's list:
@@ -178,19 +234,25 @@ enum KeyMode : int {
 
 // One split of one row: block index `bid` = row * splits + split; its
 // partials go to split slot split_base + split of splits_total per row.
-template <typename T, bool FUSED, int MODE>
+template <typename T, bool FUSED, int MODE, int W>
 __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials& part, int splits, int split_base,
                                                int splits_total, int64_t bid, int hg) {
-  __shared__ uint16_t ks[2 * kTileKeys * kKStride];   // two key tiles, row-major (the next one is stored during the current PV)
+  using S = AttnShape<W>;
+  static_assert(!FUSED || W == 8, "the fused kernel reads each host tile once for all 64 heads");
+  constexpr int kTileElems = kTileKeys * kKStride;
+  constexpr int kWindowTiles = S::kWindowTiles;
+  constexpr int kPf = S::kPf;
+  __shared__ uint16_t ks[S::kBuffers * kTileElems];  // key tiles, row-major
   __shared__ int16_t cpos[MODE == kKeysCopied ? kTopK : 1];  // kKeysCopied: list positions of the copied keys
-  __shared__ int scan_scratch[kAttnWaves + 1];
+  __shared__ int scan_scratch[W + 1];
   // Partial S of each wave (its half of the dims): 8 floats per lane.
-  __shared__ float4 s_half[kAttnWaves * 64 * 2];
+  __shared__ float4 s_half[W * 64 * 2];
   // Resolved keys of the current window of kWindowTiles tiles (one per thread):
-  // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to, flags.
-  __shared__ int64_t win_src[kWindowKeys];
-  __shared__ int64_t win_dst[kWindowKeys];
-  __shared__ __align__(16) int win_flag[kWindowKeys];  // bit 0: attend, bit 1: source is DRAM, bit 2: source valid
+  // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to (fused
+  // only), flags.
+  __shared__ int64_t win_src[S::kWindowKeys];
+  __shared__ int64_t win_dst[FUSED ? S::kWindowKeys : 1];
+  __shared__ __align__(16) int win_flag[S::kWindowKeys];  // bit 0: attend, bit 1: source is DRAM, bit 2: source valid
 
   const int64_t row = bid / splits;
   const int split = static_cast<int>(bid - row * splits);
@@ -200,8 +262,8 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const int half = wave >> 2;  // dimension half of this wave (uniform)
-  const int h0 = hg * kHeadsPerBlock + (wave & 3) * 16;
+  const int half = wave / S::kPairs;  // dimension half of this wave (uniform)
+  const int h0 = hg * S::kHeads + (wave % S::kPairs) * 16;
   const bool wave_active = h0 < a.heads;
   const int head = h0 + l16;
   const int64_t H = a.heads;
@@ -227,12 +289,13 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
 
   RowPlan plan = plan_row(a, row);
   if (MODE == kKeysCopied) {
-    // Compact the positions j < 2048 with key_src >= 0 (4 per thread, in
-    // order); the launch attends those entries only, and no tail.
+    // Compact the positions j < 2048 with key_src >= 0 (consecutive runs of
+    // kPer per thread, in order); the launch attends those entries only, and
+    // no tail.
     int n_copied = 0;
     if (plan.active && plan.sparse > 0) {
       const int32_t* ksrc = a.key_src + row * kTopK;
-      constexpr int kPer = kTopK / kAttnThreads;
+      constexpr int kPer = kTopK / S::kThreads;
       unsigned bits = 0u;
 #pragma unroll
       for (int e = 0; e < kPer; ++e)
@@ -340,31 +403,34 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
       }
     }
     win_src[tid] = src;
-    win_dst[tid] = dst;
+    if (FUSED) win_dst[tid] = dst;
     win_flag[tid] = flag;
   };
   // Two mappings of a tile's 32 x 72 chunks of 16 bytes onto the threads;
   // both fill the same row-major LDS tile.
   // * HBM tiles: thread t owns key lk = (t & 255) >> 3 and, with lg = t & 7,
   //   the chunks lg + 8j of its row (j < 8: CKV bytes [16 lg + 128 j, +16);
-  //   j = 8: KPE bytes [16 lg, +16)): threads t < 256 take j = 0..3 and the
-  //   KPE chunk, threads t >= 256 take j = 4..7 (the split is by wave, so
-  //   uniform).  One window lookup per thread and tile, immediate offsets.
+  //   j = 8: KPE bytes [16 lg, +16)).  W = 8: threads t < 256 take j = 0..3
+  //   and the KPE chunk, threads t >= 256 take j = 4..7 (the split is by
+  //   wave, so uniform); W = 4: every thread all 9.  One window lookup per
+  //   thread and tile, immediate offsets.
   // * The fused kernel (host-sourced rows): chunk c = j * 512 + t (j < 5,
   //   c < 2304), so a wave instruction reads one whole KiB of consecutive
   //   row bytes, the request shape the host link serves fastest.
   const int lk = (tid & 255) >> 3;
   const int lg = tid & 7;
+  const int ld_half = W == 8 ? (tid >> 8) : 0;  // which CKV chunks of its key the thread moves (uniform per wave)
   constexpr int kTileChunks = kTileKeys * kChunksPerKey;  // 2304
-  auto load_tile = [&](int w, bool host_tile, uint4 (&pf)[kChunksPerThread]) {
+  constexpr int kCkv = S::kCkvChunks;
+  auto load_tile = [&](int w, bool host_tile, uint4 (&pf)[kPf]) {
     if (FUSED && host_tile) {
       int t = tid;
       asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
-      for (int jj = 0; jj < kChunksPerThread; ++jj) {
+      for (int jj = 0; jj < kPf; ++jj) {
         const int cidx = jj * kAttnThreads + t;
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (jj < kChunksPerThread - 1 || cidx < kTileChunks) {  // (the last round: waves 0-3 only)
+        if (jj < kPf - 1 || cidx < kTileChunks) {  // (the last round: waves 0-3 only)
           const int k = cidx / kChunksPerKey;
           const int pc = cidx - k * kChunksPerKey;
           const int wk = w * kTileKeys + k;
@@ -383,24 +449,24 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     const int wk = w * kTileKeys + lk;
     const int flag = win_flag[wk];
     const int64_t src = win_src[wk];
-    const uint4* ckv = hbm_ckv + src * 64 + lg + 32 * half;
+    const uint4* ckv = hbm_ckv + src * 64 + lg + 8 * kCkv * ld_half;
     if (flag & 4) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) pf[j] = ckv[8 * j];
-      pf[4] = half == 0 ? hbm_kpe[src * 8 + lg] : make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < kCkv; ++j) pf[j] = ckv[8 * j];
+      pf[kCkv] = ld_half == 0 ? hbm_kpe[src * 8 + lg] : make_uint4(0, 0, 0, 0);
     } else {
 #pragma unroll
-      for (int j = 0; j < kChunksPerThread; ++j) pf[j] = make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < kPf; ++j) pf[j] = make_uint4(0, 0, 0, 0);
     }
   };
-  auto store_tile = [&](int w, bool host_tile, const uint4 (&pf)[kChunksPerThread], uint16_t* kt_base) {
+  auto store_tile = [&](int w, bool host_tile, const uint4 (&pf)[kPf], uint16_t* kt_base) {
     if (FUSED && host_tile) {
       int t = tid;
       asm volatile("" : "+v"(t));  // recompute the chunk map here (not kept live across the loop)
 #pragma unroll
-      for (int jj = 0; jj < kChunksPerThread; ++jj) {
+      for (int jj = 0; jj < kPf; ++jj) {
         const int cidx = jj * kAttnThreads + t;
-        if (jj == kChunksPerThread - 1 && cidx >= kTileChunks) break;
+        if (jj == kPf - 1 && cidx >= kTileChunks) break;
         const int k = cidx / kChunksPerKey;
         const int pc = cidx - k * kChunksPerKey;
         *reinterpret_cast<uint4*>(&kt_base[k * kKStride + pc * 8]) = pf[jj];
@@ -415,17 +481,17 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
       }
       return;
     }
-    uint16_t* rowp = &kt_base[lk * kKStride + lg * 8 + 256 * half];
+    uint16_t* rowp = &kt_base[lk * kKStride + lg * 8 + 64 * kCkv * ld_half];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(rowp + 64 * j) = pf[j];
-    if (half == 0) *reinterpret_cast<uint4*>(&kt_base[lk * kKStride + kCkvDim + lg * 8]) = pf[4];
+    for (int j = 0; j < kCkv; ++j) *reinterpret_cast<uint4*>(rowp + 64 * j) = pf[j];
+    if (ld_half == 0) *reinterpret_cast<uint4*>(&kt_base[lk * kKStride + kCkvDim + lg * 8]) = pf[kCkv];
   };
 
   // The fused kernel reads every tile row per wave: with the key-per-8-lanes
   // mapping on its HBM tiles, the host link under them served the miss tiles
   // more slowly (cfg1 fused kernel 129 -> 138 us).
   auto is_host_tile = [&](int, int) { return FUSED; };
-  uint4 pf[kChunksPerThread];
+  uint4 pf[kPf];
 
   const float qscale = a.scale * kLog2e;
   const bool compute = wave_active && plan.active;  // uniform per wave, equal within a pair
@@ -435,11 +501,13 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
 #pragma unroll
   for (int i = 0; i < kVDims / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float4* my_s = &s_half[(wave * 64 + lane) * 2];
-  const float4* pair_s = &s_half[((wave ^ 4) * 64 + lane) * 2];
+  const float4* pair_s = &s_half[((wave ^ S::kPairs) * 64 + lane) * 2];
 
-  // Per tile two barriers: (S halves written) and (next tile stored, this
-  // tile's PV done).  Tile w sits in buffer w & 1; tile w + 1 is loaded
-  // during S(w) and stored into the other buffer after PV(w)'s reads.
+  // Two buffers: per tile two barriers, (S halves written) and (next tile
+  // stored, this tile's PV done); tile w sits in buffer w & 1, tile w + 1 is
+  // loaded during S(w) and stored into the other buffer after PV(w)'s reads.
+  // One buffer: a third barrier (every wave done with tile w) before tile
+  // w + 1 is stored over it.
   for (int first = 0; first < my_tiles; first += kWindowTiles) {
     resolve_window(first);
     __syncthreads();
@@ -448,8 +516,8 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     __syncthreads();
     const int wtiles = min(kWindowTiles, my_tiles - first);
     for (int w = 0; w < wtiles; ++w) {
-      uint16_t* kcur = ks + (w & 1) * (kTileKeys * kKStride);
-      uint16_t* knext = ks + ((w + 1) & 1) * (kTileKeys * kKStride);
+      uint16_t* kcur = ks + (S::kBuffers == 2 ? (w & 1) : 0) * kTileElems;
+      uint16_t* knext = ks + (S::kBuffers == 2 ? ((w + 1) & 1) : 0) * kTileElems;
       if (w + 1 < wtiles) load_tile(w + 1, is_host_tile(first, w + 1), pf);  // in flight during S and PV below
 
       // This wave's half of the S^T tile: two 16-key blocks; lane holds
@@ -562,7 +630,10 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
           oacc[dt] = T::mfma16(af, pb_lo, T::mfma16(af, pb_hi, oacc[dt]));
         }
       }
-      if (w + 1 < wtiles) store_tile(w + 1, is_host_tile(first, w + 1), pf, knext);
+      if (w + 1 < wtiles) {
+        if constexpr (S::kBuffers == 1) __syncthreads();  // every wave done with tile w
+        store_tile(w + 1, is_host_tile(first, w + 1), pf, knext);
+      }
       __syncthreads();  // tile w + 1 resident; every wave done with tile w and s_half
     }
   }
@@ -585,12 +656,16 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   }
 }
 
-// Two waves per SIMD (one 512-thread workgroup per CU): the compiler may use
-// up to 256 registers per lane and schedule for latency, not occupancy.
-template <typename T, bool FUSED, int MODE>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void sfa_split_kernel(SfaArgs a, Partials part, int splits, int split_base,
-                                                                 int splits_total) {
-  sfa_split_body<T, FUSED, MODE>(a, part, splits, split_base, splits_total, blockIdx.x, blockIdx.y);
+// Two waves per SIMD (one 8-wave or two 4-wave workgroups per CU): the
+// compiler may use up to 256 registers per lane and schedule for latency, not
+// occupancy.  The grid's x extent may be padded past rows * splits (4-wave
+// launches: to a multiple of 8, so workgroup (x, y) shares its XCD with
+// (x, y') when the dispatcher deals linear ids round-robin over the 8 XCDs).
+template <typename T, bool FUSED, int MODE, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void sfa_split_kernel(
+    SfaArgs a, Partials part, int splits, int split_base, int splits_total) {
+  if (static_cast<int64_t>(blockIdx.x) >= a.batch * a.rows_per_request * splits) return;
+  sfa_split_body<T, FUSED, MODE, W>(a, part, splits, split_base, splits_total, blockIdx.x, blockIdx.y);
 }
 
 // MTP3 fused_copy_sfa, first launch: attention over the HBM-resident keys
@@ -620,7 +695,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   }
   const int i = slot * (8 - kCopyXcds) + (xcd - kCopyXcds);
   if (i >= attn_blocks * hgroups) return;
-  sfa_split_body<T, false, kKeysResident>(a, part, splits, 0, splits_total, i % attn_blocks, i / attn_blocks);
+  sfa_split_body<T, false, kKeysResident, 8>(a, part, splits, 0, splits_total, i % attn_blocks, i / attn_blocks);
 }
 
 // Merge split partials: one workgroup per (row, head) of G groups of 128
@@ -715,10 +790,34 @@ void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int split
   launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>, grid, dim3(128 * groups), stream, a, p, splits);
 }
 
+// One non-fused split-attention launch of plan `sp` (partials at split
+// slots [split_base, split_base + sp.splits) of `total` per row).
+template <typename T, int MODE>
+void launch_split(int kernel_id, const SfaArgs& a, const Partials& p, int64_t rows, const SplitPlan& sp,
+                  int split_base, int total, hipStream_t stream) {
+  if (sp.waves == 4)
+    launch_kernel(kernel_id, sfa_split_kernel<T, false, MODE, 4>,
+                  dim3(static_cast<uint32_t>(split_grid_x<4>(rows * sp.splits)), static_cast<uint32_t>(sp.hgroups)),
+                  dim3(AttnShape<4>::kThreads), stream, a, p, sp.splits, split_base, total);
+  else
+    launch_kernel(kernel_id, sfa_split_kernel<T, false, MODE, 8>,
+                  dim3(static_cast<uint32_t>(rows * sp.splits), static_cast<uint32_t>(sp.hgroups)),
+                  dim3(AttnShape<8>::kThreads), stream, a, p, sp.splits, split_base, total);
+}
+
 template <typename T, bool FUSED>
 hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   const int64_t rows = a.batch * a.rows_per_request;
   if (rows == 0) return hipSuccess;
+  if (!FUSED) {
+    const SplitPlan sp = plan_split(rows, a.heads);
+    const Partials p = carve(a.workspace, rows, sp.splits, a.heads);
+    launch_split<T, kKeysAll>(kKernSfaSplit, a, p, rows, sp, 0, sp.splits, stream);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_combine<T>(a, p, rows, sp.splits, stream);
+    return hipGetLastError();
+  }
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
   // From kFusedCapRows rows on, the fused kernel lasts as long as its
   // host-link-bound miss splits, so its HBM splits can take more tiles each:
@@ -731,17 +830,16 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   // -> 51.9 us, combine 4.9 -> 4.6 us, the 78-layer step 5.60 -> 5.48 ms
   // (9 splits: 5.55 ms).  With fewer rows the HBM tiles are the longer path
   // and keep every split (1 row: 64).
-  int splits = choose_splits(rows, hgroups);
-  if (FUSED && rows >= kFusedCapRows) {
+  int splits = choose_splits<8>(rows, hgroups);
+  if (rows >= kFusedCapRows) {
     const int target = rows * hgroups <= kFusedCapRows ? kFusedTargetWgsSmall : kFusedTargetWgs;
     splits = std::min<int>(splits, std::max<int>(4, std::min<int>(kFusedMaxSplits, static_cast<int>(ceil_div(
                                                                   target, rows * hgroups)))));
   }
-  SfaArgs args = a;
   const Partials p = carve(a.workspace, rows, splits, a.heads);
-  launch_kernel(FUSED ? kKernSfaSplitFused : kKernSfaSplit, sfa_split_kernel<T, FUSED, kKeysAll>,
+  launch_kernel(kKernSfaSplitFused, sfa_split_kernel<T, true, kKeysAll, 8>,
                 dim3(static_cast<uint32_t>(rows * splits), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads),
-                stream, args, p, splits, 0, splits);
+                stream, a, p, splits, 0, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_combine<T>(a, p, rows, splits, stream);
@@ -755,8 +853,9 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
   const int64_t rows = a.batch * a.rows_per_request;
   if (rows == 0) return hipSuccess;
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
+  const SplitPlan copied = plan_split(rows, a.heads);
   const int s1 = overlap_splits(rows, hgroups);
-  const int s2 = choose_splits(rows, hgroups);
+  const int s2 = copied.splits;
   const int total = s1 + s2;
   const Partials p = carve(a.workspace, rows, total, a.heads);
   ScatterArgs sc{};
@@ -782,9 +881,7 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
                 g_record_xcd_roles.load(std::memory_order_relaxed));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch_kernel(kKernSfaSplitCopied, sfa_split_kernel<T, false, kKeysCopied>,
-                dim3(static_cast<uint32_t>(rows * s2), static_cast<uint32_t>(hgroups)), dim3(kAttnThreads), stream, a,
-                p, s2, s1, total);
+  launch_split<T, kKeysCopied>(kKernSfaSplitCopied, a, p, rows, copied, s1, total, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_combine<T>(a, p, rows, total, stream);
@@ -796,8 +893,9 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
 size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens) {
   (void)max_kv_tokens;
   const int64_t hg = ceil_div(heads, kHeadsPerBlock);
-  const int64_t splits = std::max<int64_t>(choose_splits(query_rows, hg),
-                                          overlap_splits(query_rows, hg) + choose_splits(query_rows, hg));
+  const int64_t split_path = plan_split(query_rows, heads).splits;
+  const int64_t splits = std::max<int64_t>({choose_splits<8>(query_rows, hg), split_path,
+                                            overlap_splits(query_rows, hg) + split_path});
   return align256(sizeof(float) * query_rows * splits * heads * kCkvDim) +
          align256(sizeof(float) * query_rows * splits * heads * 2);
 }
