@@ -161,7 +161,18 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
   __shared__ uint16_t qs[Q * HEADS * kQStride];
   __shared__ float ws[Q * HEADS];
   __shared__ uint4 kstage[kScoreWaves * 32 * kStageStride];
-  const int b = blockIdx.y;
+  // Workgroup -> (column group, request), XCD by XCD: the dispatcher deals
+  // linear workgroup ids to the 8 XCDs in turn, and id p takes the
+  // (p mod 8)-th eighth of the grid in order, so each XCD streams a
+  // contiguous run of key blocks (when the grid divides by 8).
+  int bx = blockIdx.x, by = blockIdx.y;
+  if (((gridDim.x * gridDim.y) & 7) == 0) {
+    const int p = blockIdx.x + gridDim.x * blockIdx.y;
+    const int logical = (p & 7) * static_cast<int>((gridDim.x * gridDim.y) >> 3) + (p >> 3);
+    bx = logical % static_cast<int>(gridDim.x);
+    by = logical / static_cast<int>(gridDim.x);
+  }
+  const int b = by;
   int n = fixed_n;
   if (fixed_n < 0) {
     n = a.num_candidates[b];
@@ -171,7 +182,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
                            : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
     if (!valid) return;
   }
-  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kScoreWaves;
+  const int64_t col0 = static_cast<int64_t>(bx) * kScoreWaves;
   if (col0 * kBlock >= n) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -192,10 +203,14 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
   // row).  The query rows go to LDS once their (earlier) loads land, while
   // the key loads are still in flight.  The key block is read through a
   // buffer resource whose range is empty for an unmapped block, so those
-  // loads return zeros instead of needing a branch.  (Loading the MFMA
-  // operand layout directly -- 32 rows x 32 bytes per instruction -- has the
-  // L2 fetch ~1.4x the block's bytes from HBM.  Native vector types: uint4
-  // struct copies of these arrays stay in scratch memory.)
+  // loads return zeros instead of needing a branch.  The key loads are
+  // non-temporal: a call reads each key block once, and a model reads the
+  // layer's keys again only after every other layer has run, so keeping them
+  // in the L2 and the Infinity Cache only evicts the lines the next kernels
+  // read.  (Loading the MFMA operand layout directly -- 32 rows x 32 bytes
+  // per instruction -- has the L2 fetch ~1.4x the block's bytes from HBM.
+  // Native vector types: uint4 struct copies of these arrays stay in scratch
+  // memory.)
   constexpr int kThreads = kScoreWaves * kWave;
   constexpr int kQLoads = Q * HEADS * 16 / kThreads;
   static_assert(Q * HEADS * 16 % kThreads == 0 && Q * HEADS <= kThreads, "score staging layout");
@@ -211,7 +226,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
   u32x4_t raw[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i)  // row 4i + lane/16, chunk lane%16
-    raw[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (i * kWave + lane) * 16, 0, 0);
+    raw[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (i * kWave + lane) * 16, 0, kLoadNonTemporal);
 #pragma unroll
   for (int k = 0; k < kQLoads; ++k) {
     const int i = k * kThreads + threadIdx.x;
@@ -232,9 +247,9 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
       // at zero; the request's ceil(n / 512) workgroups share the clearing.
       const int active = static_cast<int>(ceil_div(n, kScoreWaves * kBlock));
       uint32_t* h = side.hist + static_cast<int64_t>(b) * kHistBins;
-      for (int i = static_cast<int>(blockIdx.x) * kThreads + threadIdx.x; i < kHistBins; i += active * kThreads)
+      for (int i = bx * kThreads + threadIdx.x; i < kHistBins; i += active * kThreads)
         h[i] = 0u;
-      if (blockIdx.x == 0 && threadIdx.x == 0) side.done[b] = 0;
+      if (bx == 0 && threadIdx.x == 0) side.done[b] = 0;
     }
   }
   if (!has_block) return;

@@ -39,6 +39,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // = 32 bit, everything else zero.  A buffer load whose byte offset falls
 // outside the resource's num_records returns zeros and touches no memory.
 constexpr int kBufferFlags = 0x00020000;
+// Cache-policy operand of a buffer load: nt (non-temporal; the line is not
+// kept for reuse in the L2 or the memory-side Infinity Cache).
+constexpr int kLoadNonTemporal = 2;
 
 // Element type tags: storage is 16-bit either way; MFMA flavour differs.
 struct Bf16 {
