@@ -655,6 +655,18 @@ def main() -> int:
     torch.cuda.synchronize()
     del narrow_graphs, narrow, tn
 
+    caches = cache_states(torch, np, head, ("fuse", "split"), args.steps)
+    cold_names = ("lim_score_kernel",) + MANAGE_KERNELS + ("sfa_split_kernel_fused", "scatter_copy_kernel",
+                                                           "sfa_split_kernel", "sfa_combine_kernel")
+    cold_cache = {}
+    for kind, states in caches.items():
+        for state, (step_ms, kt_c) in states.items():
+            cold_cache.setdefault(f"{kind}_eager_step", {})[state] = round(step_ms * 1000, 2)
+            for name in _ran(kt_c, cold_names):
+                key = f"{kind}:{name.replace('_kernel', '')}"
+                cold_cache.setdefault(key, {})[state] = round(kt_c.mean_ms(name) * 1000, 2)
+    del caches
+
     manage_ran = _ran(kt_fuse, MANAGE_KERNELS)
     k = {name: kt_fuse.mean_ms(name) for name in ("lim_score_kernel",) + manage_ran +
          ("sfa_split_kernel_fused", "sfa_combine_kernel")}
@@ -748,6 +760,7 @@ def main() -> int:
             "scatter_copy": round(ks["scatter_copy_kernel"] * 1000, 2), "sfa_split": round(ks["sfa_split_kernel"] * 1000, 2),
             "sfa_hbm_GBs": round(sfa_ach, 1), "measured_hbm_copy_GBs": round(hbm_copy, 1),
             "wall_us_per_step": round(wall_ms * 1000, 2),
+            "cache_states": cold_cache,
         },
         "cpu_baseline": cpu,
         "rows": rows,
@@ -760,6 +773,39 @@ def main() -> int:
 
 def _kernel_means(kt, names):
     return _kernel_table(kt, names)
+
+
+def cache_states(torch, np, head, kinds, steps: int):
+    """Eager layer-steps warm (back to back, as the timed replays run) and
+    cold: before each cold step a 1 GiB read-only pass over another buffer
+    (untimed) evicts the L2s and the 256 MB Infinity Cache.  A model reads a
+    layer's keys, HBM caches and partials again only after every other layer
+    has run, so its steps are the cold ones; one layer replayed back to back
+    keeps part of its 192 MiB of keys cached.  Both loops are instrumented the
+    same way (HIP events around each step and around each kernel).  Returns
+    {kind: {"warm"|"cold": (median step ms, KernelTimer)}}."""
+    from nanovllm_amd import _lib
+
+    dev = head.t["query"].device
+    scrub = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    acc = torch.zeros((), dtype=torch.float32, device=dev)
+    out = {}
+    for kind in kinds:
+        for state in ("warm", "cold"):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+            with _lib.KernelTimer(capacity=16 * steps) as kt:
+                for i in range(steps):
+                    if state == "cold":
+                        torch.sum(scrub, 0, out=acc)
+                    ev[i][0].record()
+                    head.step(kind, head.parity)
+                    head.parity ^= 1
+                    ev[i][1].record()
+                torch.cuda.synchronize()
+            out.setdefault(kind, {})[state] = (float(np.median([x.elapsed_time(y) for x, y in ev])), kt)
+    del scrub
+    torch.cuda.empty_cache()
+    return out
 
 
 def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
