@@ -68,8 +68,8 @@ constexpr int kMaxSplits = 64;
 //   overlap launch.
 // * W = 4: 32 heads, two workgroups per CU, one tile buffer (a third barrier
 //   per tile before the next tile is stored).  Small sparse_tail_attention
-//   and MTP3 copied-key launches (plan_split): twice the workgroups of the
-//   8-wave grid, and the two workgroups of a CU are not tied by one barrier.
+//   launches (plan_split): twice the workgroups of the 8-wave grid, and the
+//   two workgroups of a CU are not tied by one barrier.
 //   A row's two head halves read the same key tiles; they are launched on
 //   one XCD so the second read hits its L2.
 template <int W>
@@ -205,8 +205,8 @@ int choose_splits(int64_t rows, int64_t head_groups) {
   return static_cast<int>(s);
 }
 
-// Shape of a sparse_tail_attention or MTP3 copied-key launch.  4-wave
-// workgroups where the 8-wave grid leaves most CUs idle (at most two
+// Shape of a sparse_tail_attention launch.  4-wave workgroups where the
+// 8-wave grid leaves most CUs idle (at most two
 // (row, 64-head group) pairs: 64 splits each, up to 128 workgroups on 256
 // CUs), 8-wave ones otherwise.  Kernel times at 64 heads, 8 -> 4 waves:
 // 1 row 13.2 -> 10.5 us, 2 rows 15.3 -> 13.9, 3 rows 17.9 -> 17.5, 24 rows
@@ -791,18 +791,22 @@ void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int split
 }
 
 // One non-fused split-attention launch of plan `sp` (partials at split
-// slots [split_base, split_base + sp.splits) of `total` per row).
+// slots [split_base, split_base + sp.splits) of `total` per row; the
+// 4-wave shape is built for the all-keys mode only).
 template <typename T, int MODE>
 void launch_split(int kernel_id, const SfaArgs& a, const Partials& p, int64_t rows, const SplitPlan& sp,
                   int split_base, int total, hipStream_t stream) {
-  if (sp.waves == 4)
-    launch_kernel(kernel_id, sfa_split_kernel<T, false, MODE, 4>,
-                  dim3(static_cast<uint32_t>(split_grid_x<4>(rows * sp.splits)), static_cast<uint32_t>(sp.hgroups)),
-                  dim3(AttnShape<4>::kThreads), stream, a, p, sp.splits, split_base, total);
-  else
-    launch_kernel(kernel_id, sfa_split_kernel<T, false, MODE, 8>,
-                  dim3(static_cast<uint32_t>(rows * sp.splits), static_cast<uint32_t>(sp.hgroups)),
-                  dim3(AttnShape<8>::kThreads), stream, a, p, sp.splits, split_base, total);
+  if constexpr (MODE == kKeysAll) {
+    if (sp.waves == 4) {
+      launch_kernel(kernel_id, sfa_split_kernel<T, false, MODE, 4>,
+                    dim3(static_cast<uint32_t>(split_grid_x<4>(rows * sp.splits)), static_cast<uint32_t>(sp.hgroups)),
+                    dim3(AttnShape<4>::kThreads), stream, a, p, sp.splits, split_base, total);
+      return;
+    }
+  }
+  launch_kernel(kernel_id, sfa_split_kernel<T, false, MODE, 8>,
+                dim3(static_cast<uint32_t>(rows * sp.splits), static_cast<uint32_t>(sp.hgroups)),
+                dim3(AttnShape<8>::kThreads), stream, a, p, sp.splits, split_base, total);
 }
 
 template <typename T, bool FUSED>
@@ -853,7 +857,8 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
   const int64_t rows = a.batch * a.rows_per_request;
   if (rows == 0) return hipSuccess;
   const int64_t hgroups = ceil_div(a.heads, kHeadsPerBlock);
-  const SplitPlan copied = plan_split(rows, a.heads);
+  // (MTP3 has at least 4 rows: the copied keys always take the 8-wave shape.)
+  const SplitPlan copied{8, choose_splits<8>(rows, hgroups), hgroups};
   const int s1 = overlap_splits(rows, hgroups);
   const int s2 = copied.splits;
   const int total = s1 + s2;
@@ -893,9 +898,8 @@ hipError_t launch_fused_mtp(const SfaArgs& a, hipStream_t stream) {
 size_t sfa_workspace_bytes(int64_t query_rows, int64_t heads, int64_t max_kv_tokens) {
   (void)max_kv_tokens;
   const int64_t hg = ceil_div(heads, kHeadsPerBlock);
-  const int64_t split_path = plan_split(query_rows, heads).splits;
-  const int64_t splits = std::max<int64_t>({choose_splits<8>(query_rows, hg), split_path,
-                                            overlap_splits(query_rows, hg) + split_path});
+  const int64_t splits = std::max<int64_t>({choose_splits<8>(query_rows, hg), plan_split(query_rows, heads).splits,
+                                            overlap_splits(query_rows, hg) + choose_splits<8>(query_rows, hg)});
   return align256(sizeof(float) * query_rows * splits * heads * kCkvDim) +
          align256(sizeof(float) * query_rows * splits * heads * 2);
 }
