@@ -10,7 +10,9 @@ tables' natural width or the model runner's 65536-wide layout -- and runs
 LIM, then offload_fuse and offload_split, as the config tests do: LIM
 outputs, the pool and both HBM caches bit-exact, attention within the
 north-star tolerance.  The index query is guarded against near-ties at the
-selection boundary (``make_chain_case(guard=True)``).
+selection boundary (``make_chain_case(guard=True)``).  The edge draws add
+requests that are entirely cold or entirely cached, caches up to 16383 slots,
+4 to 128 heads and 64K-token prompts.
 """
 
 from __future__ import annotations
@@ -53,6 +55,29 @@ def _mtp3_shape(seed: int):
     heads = int(rng.choice([16, 64]))
     wide = bool(rng.integers(0, 2))
     return batch, lens, caches, tails, fracs, heads, wide
+
+
+def _edge_shape(seed: int):
+    """Harsher draws: whole requests cold (every selected token a miss) or fully
+    cached, cache sizes up to the 16383-slot maximum, 4 to 128 attention heads,
+    prompts up to 64K tokens; every third seed an MTP3 batch."""
+    rng = np.random.default_rng(9000 + seed)
+    mtp = seed % 3 == 2
+    batch = int(rng.integers(1, 5 if mtp else 9))
+    if mtp:
+        blocks = rng.integers(64, 257, size=batch)
+        lens = (blocks * 128).tolist()
+        caches = [int(min(L, rng.choice([8192, 12288, 16383]))) for L in lens]
+        tails = rng.integers(4, 128, size=batch).tolist()
+    else:
+        blocks = rng.integers(16, 513, size=batch)
+        lens = (blocks * 128).tolist()
+        caches = [int(min(L, rng.choice([2048, 4096, 8192, 12288, 16383]))) for L in lens]
+        tails = rng.integers(1, 128, size=batch).tolist()
+    fracs = [float(rng.choice([0.0, 0.5, 1.0])) for _ in range(batch)]
+    heads = int(rng.choice([4, 16, 64, 128]))
+    wide = bool(rng.integers(0, 2))
+    return mtp, batch, lens, caches, tails, fracs, heads, wide
 
 
 def _run(case, mtp: bool, wide: bool, tag: str) -> None:
@@ -107,3 +132,15 @@ def test_mtp3_chain_random_shape(seed):
     case = make_chain_case(batch, lens, caches, tails, attn_heads=heads, miss_fracs=fracs, seed=seed, guard=True,
                            mtp=True)
     _run(case, mtp=True, wide=wide, tag=tag)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_chain_edge_shape(seed):
+    from nanovllm_amd.workloads import make_chain_case
+
+    mtp, batch, lens, caches, tails, fracs, heads, wide = _edge_shape(seed)
+    tag = f"edge seed={seed} mtp={mtp} B={batch} heads={heads} wide={wide}"
+    print(f"{tag}: lens={lens} C={caches} miss_fracs={fracs}", flush=True)
+    case = make_chain_case(batch, lens, caches, tails, attn_heads=heads, miss_fracs=fracs, seed=seed, guard=True,
+                           mtp=mtp)
+    _run(case, mtp=mtp, wide=wide, tag=tag)
