@@ -147,6 +147,9 @@ __device__ inline void wave_minmax_to_lane63(uint32_t& lo, uint32_t& hi) {
   hi = wave_reduce_to_lane63(hi, MaxU32Op{});
 }
 
+// Tokens each score wave takes: MTP3 (Q > 1) half a key block, MTP0 a whole one.
+__host__ __device__ constexpr int score_tokens_per_wave(int q) { return q > 1 ? kBlock / 2 : kBlock; }
+
 // ---------------------------------------------------------------------------
 // 1. Scores.
 // RELU = false is the first-decode initialisation score (no ReLU,
@@ -158,9 +161,16 @@ __device__ inline void wave_minmax_to_lane63(uint32_t& lo, uint32_t& hi) {
 template <typename T, int HEADS, int Q, bool RELU>
 __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs a, float* scores, int mtp,
                                                                         int fixed_n, LimWs side) {
+  // Tokens per wave and rows per transpose stage: MTP3 waves take half a
+  // block (64 tokens) through 16-row stages, so a workgroup needs <= 53 KB of
+  // LDS and a wave <= 168 registers -- three workgroups (12 waves) per CU
+  // instead of two; MTP0 waves take a whole block through 32-row stages.
+  constexpr int kTpw = score_tokens_per_wave(Q);
+  constexpr int kStageRows = Q > 1 ? 16 : 32;
+  constexpr int kTiles = kTpw / 32;
   __shared__ uint16_t qs[Q * HEADS * kQStride];
   __shared__ float ws[Q * HEADS];
-  __shared__ uint4 kstage[kScoreWaves * 32 * kStageStride];
+  __shared__ uint4 kstage[kScoreWaves * kStageRows * kStageStride];
   // Workgroup -> (column group, request), XCD by XCD: the dispatcher deals
   // linear workgroup ids to the 8 XCDs in turn, and id p takes the
   // (p mod 8)-th eighth of the grid in order, so each XCD streams a
@@ -182,15 +192,14 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
                            : lim_row_valid(n, c, r, a.source_capacity, a.pool_rows);
     if (!valid) return;
   }
-  const int64_t col0 = static_cast<int64_t>(bx) * kScoreWaves;
-  if (col0 * kBlock >= n) return;
+  if (static_cast<int64_t>(bx) * kScoreWaves * kTpw >= n) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 5;   // k-half of the MFMA operand
   const int col_lane = lane & 31;
-  const int64_t col = col0 + wave;
-  const int64_t t0 = col * kBlock;
+  const int64_t t0 = (static_cast<int64_t>(bx) * kScoreWaves + wave) * kTpw;  // the wave's first token
+  const int64_t col = t0 / kBlock;                                              // its key block
   const bool has_block = t0 < n;
   const int32_t phys = has_block ? a.block_table[static_cast<int64_t>(b) * a.cols + col] : -1;
   const bool key_ok = has_block && phys >= 0 && phys < a.key_blocks;
@@ -220,12 +229,13 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
   for (int k = 0; k < kQLoads; ++k) qv[k] = qsrc[k * kThreads + threadIdx.x];
   const uint16_t w16 = static_cast<const uint16_t*>(a.weights)[static_cast<int64_t>(b) * Q * HEADS +
                                                                 threadIdx.x % (Q * HEADS)];
-  const char* kbase = static_cast<const char*>(a.key_cache) + (key_ok ? static_cast<int64_t>(phys) * kBlock * 256 : 0);
+  const char* kbase = static_cast<const char*>(a.key_cache) +
+                      (key_ok ? static_cast<int64_t>(phys) * kBlock * 256 + (t0 - col * kBlock) * 256 : 0);
   const __amdgpu_buffer_rsrc_t krsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbase), 0, key_ok ? kBlock * 256 : 0, kBufferFlags);
-  u32x4_t raw[32];
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbase), 0, key_ok ? kTpw * 256 : 0, kBufferFlags);
+  u32x4_t raw[kTpw / 4];
 #pragma unroll
-  for (int i = 0; i < 32; ++i)  // row 4i + lane/16, chunk lane%16
+  for (int i = 0; i < kTpw / 4; ++i)  // row 4i + lane/16, chunk lane%16
     raw[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (i * kWave + lane) * 16, 0, kLoadNonTemporal);
 #pragma unroll
   for (int k = 0; k < kQLoads; ++k) {
@@ -245,7 +255,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
     if (side.ranges != nullptr) {
       // The request's first-digit histogram and finished-chunk counter start
       // at zero; the request's ceil(n / 512) workgroups share the clearing.
-      const int active = static_cast<int>(ceil_div(n, kScoreWaves * kBlock));
+      const int active = static_cast<int>(ceil_div(n, kScoreWaves * kTpw));
       uint32_t* h = side.hist + static_cast<int64_t>(b) * kHistBins;
       for (int i = bx * kThreads + threadIdx.x; i < kHistBins; i += active * kThreads)
         h[i] = 0u;
@@ -259,30 +269,38 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
     if (side.ranges != nullptr) brange = side.ranges + static_cast<int64_t>(b) * (cap / kBlock) + col;
   if (!key_ok) {
     for (int q = 0; q < Q; ++q)
-      for (int j = lane; j < kBlock; j += kWave)
+      for (int j = lane; j < kTpw; j += kWave)
         if (t0 + j < n) srow[q * cap + t0 + j] = -FLT_MAX;
     if (brange != nullptr && lane == 0) *brange = make_uint2(score_key(-FLT_MAX), score_key(-FLT_MAX));
     return;
   }
   // Per 32-token tile, a transpose through the wave's own LDS rows into the
-  // operand layout: kb[tt][ks] = chunk 2ks+grp of row 32tt+col_lane.  Only
-  // this wave touches these rows.  A wave's LDS operations are performed in
-  // its execution order, and the stores and loads below may alias, so the
-  // compiler keeps their program order; no fence is needed (one here keeps
-  // `raw` in scratch memory).
-  uint4* st = kstage + wave * 32 * kStageStride;
-  uint4 kb[4][8];
+  // operand layout: kb[tt][ks] = chunk 2ks+grp of row 32tt+col_lane, in
+  // stages of kStageRows rows (with 16-row stages the lanes of the rows in
+  // a stage read it).  Only this wave touches these rows.  A wave's LDS
+  // operations are performed in its execution order, and the stores and
+  // loads below may alias, so the compiler keeps their program order; no
+  // fence is needed (one here keeps `raw` in scratch memory).
+  uint4* st = kstage + wave * kStageRows * kStageStride;
+  uint4 kb[kTiles][8];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < kTiles; ++tt) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) st[(4 * j + (lane >> 4)) * kStageStride + (lane & 15)] = __builtin_bit_cast(uint4, raw[tt * 8 + j]);
+    for (int r2 = 0; r2 < 32 / kStageRows; ++r2) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kb[tt][ks] = st[col_lane * kStageStride + ks * 2 + grp];
+      for (int j = 0; j < kStageRows / 4; ++j)
+        st[(4 * j + (lane >> 4)) * kStageStride + (lane & 15)] =
+            __builtin_bit_cast(uint4, raw[tt * 8 + r2 * (kStageRows / 4) + j]);
+      if (col_lane / kStageRows == r2) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) kb[tt][ks] = st[(col_lane % kStageRows) * kStageStride + ks * 2 + grp];
+      }
+    }
   }
 
 #pragma unroll 1
   for (int q = 0; q < Q; ++q) {
-    float part[4] = {0.f, 0.f, 0.f, 0.f};
+    float part[kTiles] = {};
 #pragma unroll
     for (int ht = 0; ht < HEADS / 32; ++ht) {
       float wv[16];
@@ -293,7 +311,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 16);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int tt = 0; tt < kTiles; ++tt) {
         f32x16_t acc = {};
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
@@ -309,7 +327,7 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void lim_score_kernel(LimArgs 
     }
     uint32_t klo = 0xffffffffu, khi = 0u;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
+    for (int tt = 0; tt < kTiles; ++tt) {
       float s = xor32_op(part[tt], AddOp{});  // both halves of the head reduction
       if (s == 0.f) s = 0.f;  // one zero: -0 and +0 rank equal
       const int64_t t = t0 + tt * 32 + col_lane;
@@ -2387,7 +2405,8 @@ hipError_t launch_lidu_scores(const LiduInitArgs& a, const InitWs& w, hipStream_
 template <typename T, int Q>
 hipError_t launch_lim(const LimArgs& a, hipStream_t stream) {
   const LimWs w = carve(a.workspace, a.batch, a.source_capacity, Q);
-  const dim3 grid(static_cast<uint32_t>(ceil_div(a.cols, kScoreWaves)), static_cast<uint32_t>(a.batch));
+  const dim3 grid(static_cast<uint32_t>(ceil_div(a.cols * kBlock, kScoreWaves * score_tokens_per_wave(Q))),
+                  static_cast<uint32_t>(a.batch));
   const int mtp = Q > 1 ? 1 : 0;
   const int parts = static_cast<int>(mtp_parts(a.source_capacity));
   // The chunk counts are scanned one part per thread (MTP3 pass B, MTP0's last chunk).
