@@ -82,8 +82,9 @@ struct AttnShape {
   static constexpr int kWindowTiles = kThreads / kTileKeys;  // tiles resolved per window (one key per thread)
   static constexpr int kWindowKeys = kThreads;
   // HBM tiles: 8 threads per key; a thread loads kCkvChunks 16-byte chunks of
-  // the latent row (W = 8: the waves of dim half d take chunks 4d..4d+3 of
-  // each 8; W = 4: all 8) and, in dim half 0, one of the rope part.
+  // the latent row and, where noted, one of the rope part (W = 8: threads
+  // t < 256 take chunks 0-3 of each 8 and the rope chunk, the others chunks
+  // 4-7; W = 4: every thread all 8 and the rope chunk).
   static constexpr int kCkvChunks = W == 8 ? 4 : 8;
   // Host tiles (fused, W = 8 only): 2304 16-byte chunks over 512 threads.
   static constexpr int kPf = W == 8 ? 5 : kCkvChunks + 1;  // tile chunks held per thread
@@ -206,9 +207,9 @@ int choose_splits(int64_t rows, int64_t head_groups) {
 }
 
 // Shape of a sparse_tail_attention launch.  4-wave workgroups where the
-// 8-wave grid leaves most CUs idle (at most two
-// (row, 64-head group) pairs: 64 splits each, up to 128 workgroups on 256
-// CUs), 8-wave ones otherwise.  Kernel times at 64 heads, 8 -> 4 waves:
+// 8-wave grid leaves most CUs idle (at most two (row, 64-head group) pairs:
+// 64 splits each, up to 128 workgroups on 256 CUs), 8-wave ones otherwise.
+// Kernel times at 64 heads, 8 -> 4 waves:
 // 1 row 13.2 -> 10.5 us, 2 rows 15.3 -> 13.9, 3 rows 17.9 -> 17.5, 24 rows
 // 27.3 -> 29.8.
 struct SplitPlan {
