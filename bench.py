@@ -738,6 +738,10 @@ def main() -> int:
             "bound": "hbm", "kernel": "lim_score_kernel", "achieved": round(score_ach, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(score_ach / HBM_PEAK_GBS, 4), "traffic": pmc_traffic("lim_score_kernel"),
             "algorithmic_bytes": score_bytes, "mean_us": round(k["lim_score_kernel"] * 1000, 2),
+            # the same kernel with nothing of the step cached (breakdown_us.cache_states): as in a model
+            **({"cold_mean_us": cold_cache["fuse:lim_score"]["cold"],
+                "cold_frac": round(score_bytes / (cold_cache["fuse:lim_score"]["cold"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+               if "fuse:lim_score" in cold_cache else {}),
         },
         "h2d": {
             "kernel": "sfa_split_kernel_fused", "copy_bytes": round(copy_bytes),
