@@ -62,14 +62,17 @@ constexpr int kMaxSplits = 64;
 
 // Workgroup shapes of the split attention.  W waves form W/2 pairs, one pair
 // per 16 heads (the two waves of a pair split S and the output by dims).
-// * W = 8: 64 heads, one workgroup per CU, two tile buffers (the next tile
-//   is stored during the current one's PV).  The fused kernel (each host
-//   tile is read once, so all of a row's heads share it) and the MTP3
-//   overlap launch.
-// * W = 4: 32 heads, two workgroups per CU, one tile buffer (a third barrier
-//   per tile before the next tile is stored).  Small sparse_tail_attention
-//   launches (plan_split): twice the workgroups of the 8-wave grid, and the
-//   two workgroups of a CU are not tied by one barrier.
+// Both keep two tile buffers (the next tile is stored during the current
+// one's PV).
+// * W = 8: 64 heads, one workgroup per CU.  The fused kernel (each host tile
+//   is read once, so all of a row's heads share it) and the MTP3 overlap
+//   launch.
+// * W = 4: 32 heads, two workgroups per CU (<= 80 KB of LDS each: the pair
+//   exchange of partial S uses the buffer of the next tile, which is free
+//   until that tile is stored, at the cost of a third barrier per tile).
+//   Small sparse_tail_attention launches (plan_split): twice the workgroups
+//   of the 8-wave grid, and the two workgroups of a CU are not tied by one
+//   barrier.
 //   A row's two head halves read the same key tiles; they are launched on
 //   one XCD so the second read hits its L2.
 template <int W>
@@ -78,7 +81,7 @@ struct AttnShape {
   static constexpr int kThreads = 64 * W;
   static constexpr int kPairs = W / 2;
   static constexpr int kHeads = 16 * kPairs;
-  static constexpr int kBuffers = W == 8 ? 2 : 1;
+  static constexpr bool kAliasExchange = W == 4;  // the pair exchange lives in the next tile's buffer
   static constexpr int kWindowTiles = kThreads / kTileKeys;  // tiles resolved per window (one key per thread)
   static constexpr int kWindowKeys = kThreads;
   // HBM tiles: 8 threads per key; a thread loads kCkvChunks 16-byte chunks of
@@ -206,19 +209,20 @@ int choose_splits(int64_t rows, int64_t head_groups) {
   return static_cast<int>(s);
 }
 
-// Shape of a sparse_tail_attention launch.  4-wave workgroups where the
-// 8-wave grid leaves most CUs idle (at most two (row, 64-head group) pairs:
-// 64 splits each, up to 128 workgroups on 256 CUs), 8-wave ones otherwise.
-// Kernel times at 64 heads, 8 -> 4 waves:
-// 1 row 13.2 -> 10.5 us, 2 rows 15.3 -> 13.9, 3 rows 17.9 -> 17.5, 24 rows
-// 27.3 -> 29.8.
+// Shape of a sparse_tail_attention launch: 4-wave workgroups where the
+// 8-wave grid leaves CUs idle -- at most three (row, 64-head group) pairs,
+// 64 splits each -- or where most of an 8-wave workgroup's pairs would have
+// no head (at most 8 heads); 8-wave ones otherwise.  Kernel times, 8 -> 4
+// waves: 64 heads, 1 row 11.4 -> 10.7 us, 3 rows 18.1 -> 17.1, 24 rows
+// 27.9 -> 29.4 (not taken); 4 heads, 24 rows 17.6 -> 16.0, 48 rows 29.5 ->
+// 22.4; 16 heads, 8 rows 11.7 -> 14.9 (not taken).
 struct SplitPlan {
   int waves;
   int splits;
   int64_t hgroups;
 };
 SplitPlan plan_split(int64_t rows, int64_t heads) {
-  if (rows * ceil_div(heads, kHeadsPerBlock) <= 2) {
+  if (rows * ceil_div(heads, kHeadsPerBlock) <= 3 || heads <= 8) {
     const int64_t hg = ceil_div(heads, AttnShape<4>::kHeads);
     return {4, choose_splits<4>(rows, hg), hg};
   }
@@ -243,11 +247,12 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   constexpr int kTileElems = kTileKeys * kKStride;
   constexpr int kWindowTiles = S::kWindowTiles;
   constexpr int kPf = S::kPf;
-  __shared__ uint16_t ks[S::kBuffers * kTileElems];  // key tiles, row-major
+  __shared__ __align__(16) uint16_t ks[2 * kTileElems];  // two key tiles, row-major
   __shared__ int16_t cpos[MODE == kKeysCopied ? kTopK : 1];  // kKeysCopied: list positions of the copied keys
   __shared__ int scan_scratch[W + 1];
-  // Partial S of each wave (its half of the dims): 8 floats per lane.
-  __shared__ float4 s_half[W * 64 * 2];
+  // Partial S of each wave (its half of the dims): 8 floats per lane (4-wave
+  // shape: in the next tile's buffer).
+  __shared__ float4 s_half[S::kAliasExchange ? 1 : W * 64 * 2];
   // Resolved keys of the current window of kWindowTiles tiles (one per thread):
   // source row (HBM or DRAM), HBM row a DRAM-sourced key is stored to (fused
   // only), flags.
@@ -501,14 +506,14 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   f32x4_t oacc[kVDims / 16];
 #pragma unroll
   for (int i = 0; i < kVDims / 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float4* my_s = &s_half[(wave * 64 + lane) * 2];
-  const float4* pair_s = &s_half[((wave ^ S::kPairs) * 64 + lane) * 2];
+  const int my_x = (wave * 64 + lane) * 2;
+  const int pair_x = ((wave ^ S::kPairs) * 64 + lane) * 2;
 
-  // Two buffers: per tile two barriers, (S halves written) and (next tile
-  // stored, this tile's PV done); tile w sits in buffer w & 1, tile w + 1 is
-  // loaded during S(w) and stored into the other buffer after PV(w)'s reads.
-  // One buffer: a third barrier (every wave done with tile w) before tile
-  // w + 1 is stored over it.
+  // Per tile two barriers, (S halves written) and (next tile stored, this
+  // tile's PV done); tile w sits in buffer w & 1, tile w + 1 is loaded during
+  // S(w) and stored into the other buffer after PV(w)'s reads.  With the pair
+  // exchange in that other buffer (4 waves), a third barrier after the
+  // exchange reads keeps the store off them.
   for (int first = 0; first < my_tiles; first += kWindowTiles) {
     resolve_window(first);
     __syncthreads();
@@ -517,8 +522,11 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     __syncthreads();
     const int wtiles = min(kWindowTiles, my_tiles - first);
     for (int w = 0; w < wtiles; ++w) {
-      uint16_t* kcur = ks + (S::kBuffers == 2 ? (w & 1) : 0) * kTileElems;
-      uint16_t* knext = ks + (S::kBuffers == 2 ? ((w + 1) & 1) : 0) * kTileElems;
+      uint16_t* kcur = ks + (w & 1) * kTileElems;
+      uint16_t* knext = ks + ((w + 1) & 1) * kTileElems;
+      float4* sx = S::kAliasExchange ? reinterpret_cast<float4*>(knext) : s_half;
+      float4* my_s = sx + my_x;
+      const float4* pair_s = sx + pair_x;
       if (w + 1 < wtiles) load_tile(w + 1, is_host_tile(first, w + 1), pf);  // in flight during S and PV below
 
       // This wave's half of the S^T tile: two 16-key blocks; lane holds
@@ -547,6 +555,12 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
       }
       __syncthreads();  // both halves of S written
 
+      float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+      if (compute) {
+        o0 = pair_s[0];
+        o1 = pair_s[1];
+      }
+      if constexpr (S::kAliasExchange) __syncthreads();  // every pair read before tile w + 1 is stored over them
       if (compute) {
         // The V^T operands of the whole tile are read first, so their LDS
         // latency passes under the softmax.  A operand V^T[dim][key] from the
@@ -555,7 +569,6 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
         // transposing LDS read (lane i of a 16-lane group reads dims
         // 4(i&3)..+3 of key i>>2; lane l receives the four keys' values at
         // dim l).
-        const float4 o0 = pair_s[0], o1 = pair_s[1];
         const int4 f0 = *reinterpret_cast<const int4*>(&win_flag[w * kTileKeys + 4 * g]);
         const int4 f1 = *reinterpret_cast<const int4*>(&win_flag[w * kTileKeys + 16 + 4 * g]);
         const int fl[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
@@ -631,10 +644,7 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
           oacc[dt] = T::mfma16(af, pb_lo, T::mfma16(af, pb_hi, oacc[dt]));
         }
       }
-      if (w + 1 < wtiles) {
-        if constexpr (S::kBuffers == 1) __syncthreads();  // every wave done with tile w
-        store_tile(w + 1, is_host_tile(first, w + 1), pf, knext);
-      }
+      if (w + 1 < wtiles) store_tile(w + 1, is_host_tile(first, w + 1), pf, knext);
       __syncthreads();  // tile w + 1 resident; every wave done with tile w and s_half
     }
   }
