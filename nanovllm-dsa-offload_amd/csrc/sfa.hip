@@ -99,7 +99,7 @@ constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgr
 constexpr int kFusedMaxSplits = 16;  // fused: most splits per row from kFusedCapRows rows on
 constexpr int kFusedCapRows = 8;
 constexpr int kFusedTargetWgs = 128;  // fused: workgroups per launch above kFusedCapRows rows
-constexpr int kFusedTargetWgsSmall = 96;  // fused: workgroups per launch at kFusedCapRows rows
+constexpr int kFusedTargetWgsSmall = 80;  // fused: workgroups per launch at kFusedCapRows rows
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -841,10 +841,10 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   // row at 64 heads) and their merge small while the HBM-only splits still
   // end before the copies.  Measured: 24 rows, 6 splits (10 before): combine
   // 7.0 -> 5.7 us and the step 3 us shorter (4 splits: the fused kernel 4 us
-  // longer); 8 rows, 12 splits (32, then 16 before): the fused kernel 53.5
-  // -> 51.9 us, combine 4.9 -> 4.6 us, the 78-layer step 5.60 -> 5.48 ms
-  // (9 splits: 5.55 ms).  With fewer rows the HBM tiles are the longer path
-  // and keep every split (1 row: 64).
+  // longer); 8 rows, 10 splits (32, 16, then 12 before): the 78-layer step
+  // 5.60 -> 5.48 ms at 12, then 5.30-5.33 -> 5.26-5.28 ms at 10 (combine 4.3
+  // -> 4.1 us; 9 splits: 5.38 ms, 8: 5.33-5.35 ms).  With fewer rows the HBM
+  // tiles are the longer path and keep every split (1 row: 64).
   int splits = choose_splits<8>(rows, hgroups);
   if (rows >= kFusedCapRows) {
     const int target = rows * hgroups <= kFusedCapRows ? kFusedTargetWgsSmall : kFusedTargetWgs;
