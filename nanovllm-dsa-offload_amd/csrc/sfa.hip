@@ -98,6 +98,7 @@ constexpr int kMissSplits = 2;  // fused: least splits of a row that take its ho
 constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgroups per launch
 constexpr int kFusedMaxSplits = 16;  // fused: most splits per row from kFusedCapRows rows on
 constexpr int kFusedCapRows = 8;
+constexpr int kFusedSmallSplits = 32;  // fused: most splits per row below kFusedCapRows rows
 constexpr int kFusedTargetWgs = 128;  // fused: workgroups per launch above kFusedCapRows rows
 constexpr int kFusedTargetWgsSmall = 80;  // fused: workgroups per launch at kFusedCapRows rows
 
@@ -844,8 +845,12 @@ hipError_t launch_sfa(const SfaArgs& a, hipStream_t stream) {
   // longer); 8 rows, 10 splits (32, 16, then 12 before): the 78-layer step
   // 5.60 -> 5.48 ms at 12, then 5.30-5.33 -> 5.26-5.28 ms at 10 (combine 4.3
   // -> 4.1 us; 9 splits: 5.38 ms, 8: 5.33-5.35 ms).  With fewer rows the HBM
-  // tiles are the longer path and keep every split (1 row: 64).
+  // tiles are the longer path: at most kFusedSmallSplits per row (64 before:
+  // graph-replayed steps of 20480-token rows, 1 / 2 / 4 / 6 rows, 50.8 / 58.6 /
+  // 71.7 / 82.0 -> 49.0 / 55.1 / 68.6 / 79.5 us; 16 or 24 splits at 1 row
+  // slower).
   int splits = choose_splits<8>(rows, hgroups);
+  if (rows < kFusedCapRows) splits = std::min(splits, kFusedSmallSplits);
   if (rows >= kFusedCapRows) {
     const int target = rows * hgroups <= kFusedCapRows ? kFusedTargetWgsSmall : kFusedTargetWgs;
     splits = std::min<int>(splits, std::max<int>(4, std::min<int>(kFusedMaxSplits, static_cast<int>(ceil_div(
