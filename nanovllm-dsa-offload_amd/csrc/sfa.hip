@@ -712,8 +712,9 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 
 // Merge split partials: one workgroup per (row, head) of G groups of 128
 // threads, 4 of the 512 latent dims per thread; group g merges the splits
-// [16g, 16g + 16) (G = ceil(splits / 16), at most 8), so every thread loads
-// its output slices in one round, all in flight together.  Lane s of each
+// [Bg, Bg + B) (B = 16 and G = ceil(splits / 16), at most 8; rows of at most
+// 4 or 8 splits: one group, B = 4 or 8), so every thread loads its output
+// slices in one round, all in flight together.  Lane s of each
 // wave reads split s's (m, l) (and split s + 64's), so the running max, the
 // weights exp2(m_s - max) and the softmax denominator come from one load and
 // two wave reductions (every wave computes them).  Within a group the slices
@@ -726,8 +727,9 @@ constexpr int kCombineMaxSplits = 2 * kWave;
 constexpr int kCombineMaxGroups = kCombineMaxSplits / kCombineBatch;  // 8
 static_assert(2 * kMaxSplits <= kCombineMaxSplits, "an MTP3 launch pair merges up to 2 x kMaxSplits splits");
 
-template <typename T>
+template <typename T, int B>
 __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
+  static_assert(B == 4 || B == 8 || B == kCombineBatch, "slices per thread");
   __shared__ float4 gsum[kCombineMaxGroups - 1][128];
   const int64_t H = a.heads;
   const int lane = threadIdx.x & (kWave - 1);
@@ -739,10 +741,10 @@ __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(Sf
   const float2* mlp = reinterpret_cast<const float2*>(part.ml);
   const float4* op = reinterpret_cast<const float4*>(part.o);
   constexpr int kVec = kCkvDim / 4;
-  const int s0 = grp * kCombineBatch;
-  float4 x[kCombineBatch];
+  const int s0 = grp * B;
+  float4 x[B];
 #pragma unroll
-  for (int j = 0; j < kCombineBatch; ++j)  // an index past the last split rereads it (ignored below)
+  for (int j = 0; j < B; ++j)  // an index past the last split rereads it (ignored below)
     x[j] = op[(base + min(s0 + j, splits - 1) * H) * kVec + dq];
   float2 v0 = make_float2(0.f, 0.f), v1 = v0;
   if (lane < splits) v0 = mlp[base + lane * H];
@@ -760,10 +762,10 @@ __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(Sf
   // Consumed here, unconditionally: otherwise the compiler sinks each
   // split's load into its conditional use below, one wait each.
 #pragma unroll
-  for (int j = 0; j < kCombineBatch; ++j) asm volatile("" : "+v"(x[j].x), "+v"(x[j].y), "+v"(x[j].z), "+v"(x[j].w));
+  for (int j = 0; j < B; ++j) asm volatile("" : "+v"(x[j].x), "+v"(x[j].y), "+v"(x[j].z), "+v"(x[j].w));
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int j = 0; j < kCombineBatch; ++j) {
+  for (int j = 0; j < B; ++j) {
     const int sp = s0 + j;  // uniform
     const float ws = __builtin_bit_cast(
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sp < kWave ? w0 : w1), sp & (kWave - 1)));
@@ -795,11 +797,22 @@ __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(Sf
   *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
 }
 
+// Rows of at most 4 or 8 splits take a kernel that loads only that many
+// slices per thread (a 16-slice batch rereads the last split for the rest).
 template <typename T>
 void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int splits, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(rows), static_cast<uint32_t>(a.heads));
-  const int groups = std::min<int>(kCombineMaxGroups, std::max<int>(1, static_cast<int>(ceil_div(splits, kCombineBatch))));
-  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T>, grid, dim3(128 * groups), stream, a, p, splits);
+  if (splits <= 4) {
+    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, 4>, grid, dim3(128), stream, a, p, splits);
+    return;
+  }
+  if (splits <= 8) {
+    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, 8>, grid, dim3(128), stream, a, p, splits);
+    return;
+  }
+  const int groups = std::min<int>(kCombineMaxGroups, static_cast<int>(ceil_div(splits, kCombineBatch)));
+  launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, kCombineBatch>, grid, dim3(128 * groups), stream, a, p,
+                splits);
 }
 
 // One non-fused split-attention launch of plan `sp` (partials at split
