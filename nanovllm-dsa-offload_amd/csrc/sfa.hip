@@ -713,8 +713,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 // Merge split partials: one workgroup per (row, head) of G groups of 128
 // threads, 4 of the 512 latent dims per thread; group g merges the splits
 // [Bg, Bg + B) (B = 16 and G = ceil(splits / 16), at most 8; rows of at most
-// 4 or 8 splits: one group, B = 4 or 8), so every thread loads its output
-// slices in one round, all in flight together.  Lane s of each
+// 4, 8 or 12 splits: one group, B = 4, 8 or 12), so every thread loads its
+// output slices in one round, all in flight together.  Lane s of each
 // wave reads split s's (m, l) (and split s + 64's), so the running max, the
 // weights exp2(m_s - max) and the softmax denominator come from one load and
 // two wave reductions (every wave computes them).  Within a group the slices
@@ -729,7 +729,7 @@ static_assert(2 * kMaxSplits <= kCombineMaxSplits, "an MTP3 launch pair merges u
 
 template <typename T, int B>
 __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(SfaArgs a, Partials part, int splits) {
-  static_assert(B == 4 || B == 8 || B == kCombineBatch, "slices per thread");
+  static_assert(B == 4 || B == 8 || B == 12 || B == kCombineBatch, "slices per thread");
   __shared__ float4 gsum[kCombineMaxGroups - 1][128];
   const int64_t H = a.heads;
   const int lane = threadIdx.x & (kWave - 1);
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(128 * kCombineMaxGroups) void sfa_combine_kernel(Sf
   *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
 }
 
-// Rows of at most 4 or 8 splits take a kernel that loads only that many
+// Rows of at most 4, 8 or 12 splits take a kernel that loads only that many
 // slices per thread (a 16-slice batch rereads the last split for the rest).
 template <typename T>
 void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int splits, hipStream_t stream) {
@@ -808,6 +808,10 @@ void launch_combine(const SfaArgs& a, const Partials& p, int64_t rows, int split
   }
   if (splits <= 8) {
     launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, 8>, grid, dim3(128), stream, a, p, splits);
+    return;
+  }
+  if (splits <= 12) {
+    launch_kernel(kKernSfaCombine, sfa_combine_kernel<T, 12>, grid, dim3(128), stream, a, p, splits);
     return;
   }
   const int groups = std::min<int>(kCombineMaxGroups, static_cast<int>(ceil_div(splits, kCombineBatch)));
