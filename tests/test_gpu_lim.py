@@ -379,6 +379,45 @@ def test_lim_row_guards():
     assert np.all(ints(d["topk_src_ids"]) == -1)
 
 
+def test_lim_mtp_row_guards():
+    """MTP3 row guards (fused_li_manage_mtp_kernel.h:218-233, plus C <= 16383,
+    the 14-bit slot payload): a disabled request gets miss_counts = 0 and
+    nothing else is written -- its four query rows, its miss lists and its
+    pool row keep what they held.  Disabled here: N < 2048, C < min(N, 8192),
+    C = N = 16384 (above 16383), C > N, a pool row out of range; the last
+    request is valid and bit-exact against the oracle."""
+    from nanovllm_amd.workloads import make_chain_case
+
+    B = 6
+    case = make_chain_case(B, 16384, 8192, 8, seed=4, mtp=True, guard=False)
+    t = case.tensors
+    t["num_candidate_tokens"][0] = 1024       # N < 2048
+    t["num_cache_tokens"][1] = 4096           # C < min(N, 8192)
+    t["num_cache_tokens"][2] = 16384          # C = N above the 16383-slot maximum
+    t["num_candidate_tokens"][3] = 8064       # C = 8192 > N
+    t["req_pool_entries"][4] = 99             # pool row out of range
+    expect = oracle_lim(case, mtp=True)
+    assert expect["miss_counts"][:5].tolist() == [0] * 5 and expect["miss_counts"][5] > 0
+    d = case.to_device("cuda", host_mapped=False)
+    dt = d.tensors
+    for k in ("topk_src_ids", "topk_dst_slots", "miss_src_ids", "miss_dst_slots", "miss_counts"):
+        dt[k].fill_(-5)
+    print("LIM MTP3 row guards", flush=True)
+    _run_lim(d, mtp=True)
+    mc = ints(dt["miss_counts"])
+    assert mc.tolist() == expect["miss_counts"].tolist()
+    assert np.array_equal(ints(dt["cache_slots_pool"]), expect["pool"])
+    src = ints(dt["topk_src_ids"]).reshape(B, 4, -1)
+    dst = ints(dt["topk_dst_slots"]).reshape(B, 4, -1)
+    assert np.all(src[:5] == -5) and np.all(dst[:5] == -5)
+    assert np.array_equal(src[5], expect["src"].reshape(B, 4, -1)[5])
+    assert np.array_equal(dst[5], expect["dst"].reshape(B, 4, -1)[5])
+    ms, md = ints(dt["miss_src_ids"]), ints(dt["miss_dst_slots"])
+    assert np.all(ms[:5] == -5) and np.all(md[:5] == -5)
+    assert np.array_equal(ms[5, :mc[5]], expect["miss_src"][5, :mc[5]])
+    assert np.array_equal(md[5, :mc[5]], expect["miss_dst"][5, :mc[5]])
+
+
 def test_lim_meta_and_errors():
     from nanovllm_amd import dsa_offload_ops as ops
 

@@ -49,7 +49,8 @@ def _mtp3_shape(seed: int):
     batch = int(rng.integers(1, 5))
     blocks = rng.integers(64, 129, size=batch)  # 8192 .. 16384 tokens
     lens = (blocks * 128).tolist()
-    caches = [int(rng.choice([8192, L])) for L in lens]  # MTP3 rows need C >= min(N, 8192)
+    # MTP3 rows need C >= min(N, 8192), and C <= 16383 (the guards' tests cover the rest)
+    caches = [int(min(rng.choice([8192, L]), 16383)) for L in lens]
     tails = rng.integers(4, 128, size=batch).tolist()
     fracs = rng.uniform(0.0, 0.3, size=batch).tolist()
     heads = int(rng.choice([16, 64]))
