@@ -96,6 +96,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxSlack = 8.f;  // base-2 headroom of the running max (P < 256)
 constexpr int kMissSplits = 2;  // fused: least splits of a row that take its host-sourced tiles
 constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgroups per launch
+constexpr int kMissTilesPerSplit = 6;  // fused, launches of kMissRuleRows rows and 6 splits on: miss tiles per miss split
+constexpr int kMissRuleRows = 16;
 constexpr int kFusedMaxSplits = 16;  // fused: most splits per row from kFusedCapRows rows on
 constexpr int kFusedCapRows = 8;
 constexpr int kFusedSmallSplits = 32;  // fused: most splits per row below kFusedCapRows rows
@@ -335,17 +337,32 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   int t_first = split, t_stride = splits, t_end = ntiles;
   const int mtiles = FUSED ? static_cast<int>(ceil_div(copy_count, kTileKeys)) : 0;
   if (FUSED && mtiles > 0 && splits >= 2) {  // (one split per row takes every tile)
-    // About kMissWorkgroups workgroups of the launch take host-sourced tiles:
-    // at least kMissSplits per row (measured best at 24 rows; more of them
-    // leave too few splits for the row's HBM-resident tiles), more per row at
-    // small batches (4 at 8 rows: 3% off the 78-layer step), never more than
-    // the row's miss tiles.  A row with more than 4 miss tiles per miss split
-    // gets a third one when it has at least 6 splits: its miss workgroups
-    // were the launch's last to finish (24 rows: fused kernel -0.8 us).
-    int miss_splits = static_cast<int>(ceil_div(kMissWorkgroups, a.batch * a.rows_per_request));
-    if (miss_splits > mtiles) miss_splits = mtiles;
-    if (miss_splits < kMissSplits) miss_splits = kMissSplits;
-    if (splits >= 6 && mtiles > 4 * kMissSplits && miss_splits < 3) miss_splits = 3;
+    // Launches of kMissRuleRows rows or more with at least 6 splits per row:
+    // one miss split per kMissTilesPerSplit miss tiles of the row (1 or 2 at
+    // cfg1's 3-10 miss tiles).  Every miss workgroup keeps a whole tile of
+    // host reads in flight, and 2-3 per row queued ~8x the link's
+    // bandwidth-delay product: the link served some workgroups' first tile
+    // after ~85 us, and the HBM-only workgroups on the same XCDs, their reads
+    // stalled behind the host reads, ended last (115-124 us against ~110 us
+    // for the copies).  24 rows: the fused kernel 116-119 -> 109-110 us and
+    // the step 185.0 / 185.4 -> 178.1 / 178.7 us (4, 8 or 12 tiles per miss
+    // split: 179.8-181.3, 180.0, 180.5 us).  Smaller launches: about
+    // kMissWorkgroups workgroups take host-sourced tiles, at least kMissSplits
+    // per row, more per row at small batches (4 at 8 rows: 3% off the
+    // 78-layer step), never more than the row's miss tiles; with at least 6
+    // splits a row with more than 4 miss tiles per miss split gets a third.
+    // (64 rows of 4 splits kept this rule: the per-row one made the cfg2
+    // step 492 / 498 -> 502 / 505 us.)
+    const int64_t launch_rows = a.batch * a.rows_per_request;
+    int miss_splits;
+    if (launch_rows >= kMissRuleRows && splits >= 6) {
+      miss_splits = static_cast<int>(ceil_div(mtiles, kMissTilesPerSplit));
+    } else {
+      miss_splits = static_cast<int>(ceil_div(kMissWorkgroups, launch_rows));
+      if (miss_splits > mtiles) miss_splits = mtiles;
+      if (miss_splits < kMissSplits) miss_splits = kMissSplits;
+      if (splits >= 6 && mtiles > 4 * kMissSplits && miss_splits < 3) miss_splits = 3;
+    }
     if (miss_splits > splits - 1) miss_splits = splits - 1;
     if (split < miss_splits) {
       t_first = split;
