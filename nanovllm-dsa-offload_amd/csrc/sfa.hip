@@ -96,7 +96,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxSlack = 8.f;  // base-2 headroom of the running max (P < 256)
 constexpr int kMissSplits = 2;  // fused: least splits of a row that take its host-sourced tiles
 constexpr int kMissWorkgroups = 32;  // fused: target number of host-tile workgroups per launch
-constexpr int kMissTilesPerSplit = 6;  // fused, launches of kMissRuleRows rows and 6 splits on: miss tiles per miss split
+// Fused, launches of kMissRuleRows rows or more: miss tiles per miss split
+// (rows of at least 6 splits / fewer).
+constexpr int kMissTilesPerSplit = 6;
+constexpr int kMissTilesPerSplitFew = 12;
 constexpr int kMissRuleRows = 16;
 constexpr int kFusedMaxSplits = 16;  // fused: most splits per row from kFusedCapRows rows on
 constexpr int kFusedCapRows = 8;
@@ -337,9 +340,11 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
   int t_first = split, t_stride = splits, t_end = ntiles;
   const int mtiles = FUSED ? static_cast<int>(ceil_div(copy_count, kTileKeys)) : 0;
   if (FUSED && mtiles > 0 && splits >= 2) {  // (one split per row takes every tile)
-    // Launches of kMissRuleRows rows or more with at least 6 splits per row:
-    // one miss split per kMissTilesPerSplit miss tiles of the row (1 or 2 at
-    // cfg1's 3-10 miss tiles).  Every miss workgroup keeps a whole tile of
+    // Launches of kMissRuleRows rows or more: one miss split per
+    // kMissTilesPerSplit miss tiles of the row (1 or 2 at cfg1's 3-10 miss
+    // tiles), per kMissTilesPerSplitFew with fewer than 6 splits per row (1 at
+    // 64 rows of 4 splits, cfg2: step 485.8 / 488.1 -> 482.1 / 480.7 us; 6
+    // tiles there: 498.8 / 503.1 us).  Every miss workgroup keeps a whole tile of
     // host reads in flight, and 2-3 per row queued ~8x the link's
     // bandwidth-delay product: the link served some workgroups' first tile
     // after ~85 us, and the HBM-only workgroups on the same XCDs, their reads
@@ -351,12 +356,10 @@ __device__ __forceinline__ void sfa_split_body(const SfaArgs& a, const Partials&
     // per row, more per row at small batches (4 at 8 rows: 3% off the
     // 78-layer step), never more than the row's miss tiles; with at least 6
     // splits a row with more than 4 miss tiles per miss split gets a third.
-    // (64 rows of 4 splits kept this rule: the per-row one made the cfg2
-    // step 492 / 498 -> 502 / 505 us.)
     const int64_t launch_rows = a.batch * a.rows_per_request;
     int miss_splits;
-    if (launch_rows >= kMissRuleRows && splits >= 6) {
-      miss_splits = static_cast<int>(ceil_div(mtiles, kMissTilesPerSplit));
+    if (launch_rows >= kMissRuleRows) {
+      miss_splits = static_cast<int>(ceil_div(mtiles, splits >= 6 ? kMissTilesPerSplit : kMissTilesPerSplitFew));
     } else {
       miss_splits = static_cast<int>(ceil_div(kMissWorkgroups, launch_rows));
       if (miss_splits > mtiles) miss_splits = mtiles;
