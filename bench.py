@@ -887,8 +887,11 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
 
 
 def _graph_step_us(torch, fns, reps, prepare=None):
-    """Mean µs per replay of HIP graphs captured from ``fns`` (replayed in
-    turn); ``prepare()`` runs before each replay, outside the timed span."""
+    """Median µs per replay of HIP graphs captured from ``fns`` (replayed in
+    turn) after three untimed replays of each; ``prepare()`` runs before each
+    replay, outside the timed span.  (Every replay is timed on its own after a
+    synchronisation, so a short graph's first replays after an idle host wait
+    run long; the median keeps those out.)"""
     stream = torch.cuda.Stream()
     graphs = []
     with torch.cuda.stream(stream):
@@ -905,7 +908,12 @@ def _graph_step_us(torch, fns, reps, prepare=None):
                 f()
             graphs.append(g)
     torch.cuda.synchronize()
-    total_ms = 0.0
+    for i in range(3 * len(graphs)):
+        if prepare:
+            prepare()
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    times = []
     for i in range(reps):
         if prepare:
             prepare()
@@ -914,8 +922,9 @@ def _graph_step_us(torch, fns, reps, prepare=None):
         graphs[i % len(graphs)].replay()
         e1.record()
         torch.cuda.synchronize()
-        total_ms += e0.elapsed_time(e1)
-    return total_ms / reps * 1000
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    return times[len(times) // 2] * 1000
 
 
 def measure_cfg2(torch, np, dev, seed: int, steps: int = 10):
