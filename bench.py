@@ -887,11 +887,13 @@ def measure_mtp3(torch, np, dev, seed: int, reps: int = 8):
 
 
 def _graph_step_us(torch, fns, reps, prepare=None):
-    """Median µs per replay of HIP graphs captured from ``fns`` (replayed in
-    turn) after three untimed replays of each; ``prepare()`` runs before each
-    replay, outside the timed span.  (Every replay is timed on its own after a
-    synchronisation, so a short graph's first replays after an idle host wait
-    run long; the median keeps those out.)"""
+    """µs per replay of HIP graphs captured from ``fns`` (replayed in turn)
+    after three untimed replays of each.  Without ``prepare`` the replays run
+    back to back in windows of ``len(fns)`` x 4 between two events, and the
+    median window counts (a short graph timed alone after a synchronisation
+    runs on clocks that have dropped while the host waited); with it,
+    ``prepare()`` runs before each replay outside the timed span, each replay
+    is timed on its own, and the median replay counts."""
     stream = torch.cuda.Stream()
     graphs = []
     with torch.cuda.stream(stream):
@@ -914,15 +916,25 @@ def _graph_step_us(torch, fns, reps, prepare=None):
         graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
     times = []
-    for i in range(reps):
-        if prepare:
+    if prepare is None:
+        per = 4 * len(graphs)
+        for _ in range(max(1, reps // per)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(per):
+                graphs[i % len(graphs)].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / per)
+    else:
+        for i in range(reps):
             prepare()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        graphs[i % len(graphs)].replay()
-        e1.record()
-        torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graphs[i % len(graphs)].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
     times.sort()
     return times[len(times) // 2] * 1000
 
