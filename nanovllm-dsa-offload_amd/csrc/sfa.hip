@@ -194,8 +194,10 @@ int64_t split_grid_x(int64_t n) {
 }
 
 int overlap_splits(int64_t rows, int64_t head_groups) {
-  // About two workgroups per attention CU: the rows' tiles spread evenly.
-  int64_t s = ceil_div(2 * (8 - kCopyXcds) * 32, rows * head_groups);
+  // About one workgroup per two attention CUs: the resident keys' attention
+  // stays hidden under the copy, and the combine merges fewer partials (cfg3,
+  // 64 rows: one split per row instead of three, combine 10.45 -> 8.6 us).
+  int64_t s = ceil_div((8 - kCopyXcds) * 16, rows * head_groups);
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
   return static_cast<int>(s);
