@@ -884,6 +884,96 @@ __device__ __forceinline__ SelectOut row_threshold(const float* s, int n, int64_
         }
       }
     block_minmax(lo, hi, red);
+    // The first digit pass and, when the k-th largest key's bin holds at most
+    // kGatherKeys keys, its ranking among them.  The counting pass has no
+    // branch per key (the general passes below test each key's prefix and
+    // bounds under an exec mask): chunks wholly past n are skipped, and a key
+    // past n in the last chunk counts into one of kWave bins past kBins (by
+    // lane, against same-address contention), which no scan reads.  The same bins, ranks and outputs as radix_select_visit.
+    if (hi != lo) {
+      const int L = 32 - __clz(static_cast<int>(hi - lo));
+      const int sh = L > kDigitBits ? L - kDigitBits : 0;
+      // (An opaque copy of lo: the compiler would otherwise keep every key's
+      // difference key - lo from this pass for the later ones, 128 registers.)
+      uint32_t lo1 = lo;
+      asm volatile("" : "+s"(lo1));
+#pragma unroll
+      for (int ch = 0; ch < RES; ++ch) {
+        if (ch * kChunk >= n) break;  // (uniform)
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) {
+          const bool in = ch * kChunk + tid * kItems + e < n;
+          atomicAdd(&hist[in ? (u[ch][e] - lo1) >> sh : kBins + (tid & (kWave - 1))], 1u);
+        }
+      }
+      __syncthreads();
+      // Thread tid owns bins [tb kBinsPerThread, +kBinsPerThread), tb = 511 - tid:
+      // ascending threads scan descending bins.
+      const int tb = kManageThreads - 1 - tid;
+      int cnt[kBinsPerThread];
+      int sum = 0;
+#pragma unroll
+      for (int j = 0; j < kBinsPerThread; ++j) {
+        cnt[j] = static_cast<int>(hist[tb * kBinsPerThread + j]);
+        hist[tb * kBinsPerThread + j] = 0u;
+        sum += cnt[j];
+      }
+      if (tid < kWave) hist[kBins + tid] = 0u;
+      int total;
+      int acc = block_exclusive_scan(sum, scratch, &total);
+      if (acc < kTopK && kTopK <= acc + sum) {
+#pragma unroll
+        for (int j = kBinsPerThread - 1; j >= 0; --j) {
+          if (acc < kTopK && kTopK <= acc + cnt[j]) {
+            bcast[0] = tb * kBinsPerThread + j;
+            bcast[1] = acc;
+            bcast[2] = cnt[j];
+          }
+          acc += cnt[j];
+        }
+      }
+      __syncthreads();
+      const uint32_t bin = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bcast[0]));
+      const int remaining = kTopK - __builtin_amdgcn_readfirstlane(bcast[1]);
+      const int inbin = __builtin_amdgcn_readfirstlane(bcast[2]);
+      __syncthreads();  // bcast is reused
+      if (inbin <= kGatherKeys) {
+        if (tid == 0) bcast[3] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int ch = 0; ch < RES; ++ch)
+#pragma unroll
+          for (int e = 0; e < kItems; ++e) {
+            const uint32_t d = u[ch][e] - lo;
+            if (ch * kChunk + tid * kItems + e < n && (d >> sh) == bin)
+              hist[atomicAdd(&bcast[3], 1)] = d;  // at most inbin <= kGatherKeys entries
+          }
+        __syncthreads();
+        if (tid < kWave) {
+          const uint32_t mine = tid < inbin ? hist[tid] : 0u;
+          int greater = 0, equal = 0;
+          for (int j = 0; j < inbin; ++j) {
+            const uint32_t o = hist[j];
+            greater += o > mine ? 1 : 0;
+            equal += o == mine ? 1 : 0;
+          }
+          if (tid < inbin && greater < remaining && remaining <= greater + equal) {  // lanes holding the answer
+            bcast[0] = static_cast<int>(mine);
+            bcast[1] = remaining - greater;
+            bcast[2] = equal;
+          }
+        }
+        __syncthreads();
+        const uint32_t x = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bcast[0]));
+        const int need = __builtin_amdgcn_readfirstlane(bcast[1]);
+        const int eq = __builtin_amdgcn_readfirstlane(bcast[2]);
+        if (tid < kGatherKeys) hist[tid] = 0u;  // zero again for the next call
+        __syncthreads();
+        return SelectOut{x + lo, need, eq};
+      }
+      // More than kGatherKeys keys in the bin (heavy ties): the general passes
+      // from the start (the histogram is zero again).
+    }
     return radix_select_visit(
         kTopK, lo, hi,
         [&](auto&& fn) {
@@ -920,7 +1010,7 @@ __device__ __forceinline__ SelectOut row_threshold(const float* s, int n, int64_
 // keeps the row's keys in registers (RES chunks of 4096 tokens).
 template <int RES>
 __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a, LimWs w, int queries, int min_n) {
-  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t hist[kBins + kWave];  // (+ the bins that keys past n count into)
   __shared__ int scratch[kManageThreads / 64 + 1];
   __shared__ uint32_t red[2 * (kManageThreads / 64) + 2];
   __shared__ int bcast[4];
@@ -935,7 +1025,7 @@ __global__ __launch_bounds__(kManageThreads) void lim_threshold_kernel(LimArgs a
   if (!valid || n < min_n) return;
   const int64_t cap = a.source_capacity;
   const float* s = w.scores + (static_cast<int64_t>(b) * queries + q) * cap;
-  for (int i = tid; i < kBins; i += kManageThreads) hist[i] = 0u;
+  for (int i = tid; i < kBins + kWave; i += kManageThreads) hist[i] = 0u;
   const SelectOut sel = row_threshold<RES>(s, n, cap, hist, scratch, bcast, red);
   // Ties at the threshold go to the lowest tokens: a token with key ==
   // thresh is selected iff token <= cutoff (INT_MAX when all ties are taken).
